@@ -1,0 +1,87 @@
+/* qe_attn.h -- C ABI of the MI355X (gfx950) gated-attention decode path.
+ *
+ * Library: qengine_amd/libqe_attn.so (hand-written HIP kernels for gfx950 + this C ABI).
+ * Every entry point takes raw device pointers, row strides in elements and a HIP stream. It
+ * enqueues work on that stream and returns without a host sync. It allocates nothing, so calls
+ * can be captured in a hipGraph. `pos` is a device int32 scalar (element 0 = position of row 0),
+ * read on the device. Tensors are bf16 (`void*`) unless typed otherwise.
+ *
+ * Return value: hipSuccess, hipErrorInvalidValue for arguments outside the supported ranges
+ * (checked on the host before any launch), or the launch error reported by the HIP runtime.
+ *
+ * Shapes (head_dim D = 256 is fixed, as in the reference):
+ *   qg rows   [n][ldp]: per q head h, [q (D) | gate (D)]  -> row width Hq*2*D
+ *   k, v rows [n][ldp]: Hkv*D each (same row stride as qg)
+ *   q         [n][Hq*D] contiguous rows
+ *   kc, vc    [Hkv][max_len][D] (KV cache, updated in place by qe_attn_prep)
+ *   part_o    fp32 [>= n][Hq][NS][D], part_ml fp32 [>= n][Hq][NS][2]: caller-owned scratch
+ *             whose contents are private to this library
+ *   out rows  [n][ldo]: Hq*D
+ * Concurrency: part_o/part_ml are scratch. Two calls that share them must not overlap (as in
+ * the reference, where every layer reuses one pair).
+ */
+#ifndef QE_ATTN_H
+#define QE_ATTN_H
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* q/k RMSNorm1p (eps, weights qnw/knw, one bf16 rounding) + partial rotate-half RoPE on the first
+ * rd = 2*len(inv_freq) dims (fp32 angle pos*inv_freq, bf16 cos/sin, every op rounded to bf16).
+ * Writes q_out[t], and kc/vc[h][pos+t] when pos+t < max_len. Valid: n >= 1, Hq % Hkv == 0,
+ * 0 < rd <= 256, rd even, ldp % 8 == 0.
+ * Replaces launch_attn_prep (reference csrc/ops.h:25-27, csrc/attn.cu:157-163). */
+hipError_t qe_attn_prep(const void* qg, const void* k, const void* v, long ldp, const void* qnw,
+                        const void* knw, const float* inv_freq, const int* pos, void* q_out,
+                        void* kc, void* vc, int n, int Hq, int Hkv, int max_len, int rd,
+                        float eps, hipStream_t stream);
+
+/* Gated flash-decoding: row t attends cache positions [0, min(pos+t+1, max_len)), scores scaled
+ * by `scale`, and out[t] = bf16(bf16(softmax . V) * bf16(sigmoid(gate))), gate = qg[t][h][D:2D].
+ * Two launches: split-KV partials over fixed slices of qe_attn_split_size(max_len, NS)
+ * positions, then a log-sum-exp combine with the fused sigmoid gate. Row t of an n-row call is
+ * bit-identical to a 1-row call at position pos+t. Valid: 1 <= n <= 8, Hq % Hkv == 0,
+ * (Hq/Hkv)*n <= 64, NS >= 1, max_len*512 < 2^32, 16-byte aligned q/kc/vc.
+ * Replaces launch_attn_decode (reference csrc/ops.h:28-30, csrc/attn.cu:165-172). */
+hipError_t qe_attn_decode(const void* q, const void* kc, const void* vc, const int* pos,
+                          const void* qg, long ldp, float* part_o, float* part_ml, void* out,
+                          long ldo, int n, int Hq, int Hkv, int max_len, int NS, float scale,
+                          hipStream_t stream);
+
+/* First half of qe_attn_decode: the split-KV partials only (part_o/part_ml filled for the slices
+ * that hold positions). The pair is exported separately so that a sequence-sharded caller can
+ * exchange partials between devices before combining, and so the partials kernel can be timed
+ * on its own. No counterpart in the reference (there the pair is one launcher,
+ * csrc/attn.cu:165-172). */
+hipError_t qe_attn_decode_partials(const void* q, const void* kc, const void* vc, const int* pos,
+                                   float* part_o, float* part_ml, int n, int Hq, int Hkv,
+                                   int max_len, int NS, float scale, hipStream_t stream);
+
+/* Second half of qe_attn_decode: log-sum-exp combine of the partials + sigmoid output gate.
+ * No counterpart in the reference (see qe_attn_decode_partials). */
+hipError_t qe_attn_decode_combine(const float* part_o, const float* part_ml, const int* pos,
+                                  const void* qg, long ldp, void* out, long ldo, int n, int Hq,
+                                  int max_len, int NS, hipStream_t stream);
+
+/* Number of cache positions per split-KV slice for a cache of max_len positions and NS partial
+ * slots: a multiple of 32, at least ceil(max_len/NS). It depends only on (max_len, NS), so the
+ * slices are the same for every row and every call on the same buffers.
+ * No counterpart in the reference (its slice size depends on each row's length, attn.cu:79). */
+int qe_attn_split_size(int max_len, int NS);
+
+/* Version string of this library. */
+const char* qe_attn_version(void);
+
+/* Import-compatibility no-ops for the reference's programmatic-dependent-launch switches
+ * (reference csrc/ops.h:34-35, csrc/bindings.cpp:195-196). gfx950 has no equivalent. */
+void qe_set_pdl_trigger(int on);
+void qe_set_pdl_launch(int on);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QE_ATTN_H */

@@ -1,0 +1,14 @@
+"""CPU oracle for the gated-attention decode path. TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import this package. They use it as the checker or as the CPU baseline. It is never the thing
+measured or shipped. The product path (``qengine_amd``) never imports it, and it fails loudly
+when its HIP library is missing instead of falling back to the CPU.
+
+Parity status per function (each is pinned by checks in ``tests/test_oracle.py``):
+  rope_inv_freq, rope_cos_sin, apply_rope, rmsnorm1p, attention_qkv_from_proj,
+  attention_core, attention_core_grouped, attn_prep, attn_decode, attn_prefill,
+  flash_decode_fp64                                   -> pinned (closed forms, brute force,
+                                                         invariants, bf16 rounding model)
+"""
+from .attn_oracle import *  # noqa: F401,F403

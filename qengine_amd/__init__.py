@@ -1,0 +1,49 @@
+"""qengine_amd: MI355X-native (gfx950) gated-attention decode path for qengine.
+
+``qengine_amd._C`` exposes the reference's ``qengine._C`` attention ops with the same signatures
+(``attn_prep``, ``attn_decode``, plus the PDL switches as no-ops), backed by hand-written HIP
+kernels in ``libqe_attn.so`` (C ABI: ``include/qe_attn.h``). There is no CPU fallback: importing
+this package fails if the native libraries are not built.
+"""
+from __future__ import annotations
+
+import math
+
+# torch first: it loads its own HIP runtime, and our libraries then bind to that same copy
+# (both are named libamdhip64.so.7).
+import torch  # noqa: F401
+
+try:
+    from . import _C  # noqa: F401
+except ImportError as exc:  # pragma: no cover - exercised only on an unbuilt tree
+    raise ImportError(
+        "qengine_amd native extension is not built; run `python qengine_amd/_build.py`"
+    ) from exc
+
+from ._C import (  # noqa: E402,F401
+    attn_decode,
+    attn_decode_combine,
+    attn_decode_partials,
+    attn_prep,
+    set_pdl_launch,
+    set_pdl_trigger,
+    split_size,
+    version,
+)
+
+HEAD_DIM = 256
+TARGET_SLICE = 256  # cache positions per split-KV slice the default split count aims for
+
+
+def default_splits(max_len: int, target_slice: int = TARGET_SLICE) -> int:
+    """Split count NS (part_o.size(2)) giving slices of about ``target_slice`` positions for a
+    cache of ``max_len`` positions. NS is fixed when the scratch is allocated, so graphs stay
+    static; slices beyond the attended length cost nothing."""
+    return max(1, math.ceil(max_len / target_slice))
+
+
+def alloc_partials(n_rows: int, hq: int, ns: int, device="cuda"):
+    """Caller-owned split-KV scratch (part_o, part_ml) for up to ``n_rows`` rows."""
+    po = torch.empty(n_rows, hq, ns, HEAD_DIM, dtype=torch.float32, device=device)
+    pml = torch.empty(n_rows, hq, ns, 2, dtype=torch.float32, device=device)
+    return po, pml

@@ -1,0 +1,98 @@
+"""ctypes binding of the C ABI in include/qe_attn.h (libqe_attn.so), without the torch extension.
+
+This is the binding a non-torch host (or a test that must go through the C ABI) uses. Tensor
+arguments may be torch tensors (their data_ptr is passed) or raw integer device addresses.
+Streams are raw hipStream_t values (0 = the null stream; torch:
+``torch.cuda.current_stream().cuda_stream``).
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch  # noqa: F401  (loads torch's HIP runtime first; see qengine_amd/__init__.py)
+
+LIB_PATH = Path(__file__).resolve().parent / "libqe_attn.so"
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_long
+_F = ctypes.c_float
+
+SIGNATURES = {
+    "qe_attn_prep": (_I, [_P, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P]),
+    "qe_attn_decode": (_I, [_P, _P, _P, _P, _P, _L, _P, _P, _P, _L, _I, _I, _I, _I, _I, _F, _P]),
+    "qe_attn_decode_partials": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P]),
+    "qe_attn_decode_combine": (_I, [_P, _P, _P, _P, _L, _P, _L, _I, _I, _I, _I, _P]),
+    "qe_attn_split_size": (_I, [_I, _I]),
+    "qe_attn_version": (ctypes.c_char_p, []),
+    "qe_set_pdl_trigger": (None, [_I]),
+    "qe_set_pdl_launch": (None, [_I]),
+}
+
+HIP_SUCCESS = 0
+HIP_ERROR_INVALID_VALUE = 1
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libqe_attn.so and declare every exported entry point (raises if it is not built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise OSError(f"{LIB_PATH} is not built; run `python qengine_amd/_build.py`")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def _ptr(x) -> int | None:
+    if x is None:
+        return None
+    return x.data_ptr() if hasattr(x, "data_ptr") else int(x)
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    return int(stream)
+
+
+def prep(qg, k, v, ldp, qnw, knw, inv_freq, pos, q_out, kc, vc, n, hq, hkv, max_len, rd, eps,
+         stream=None) -> int:
+    return load().qe_attn_prep(_ptr(qg), _ptr(k), _ptr(v), ldp, _ptr(qnw), _ptr(knw),
+                               _ptr(inv_freq), _ptr(pos), _ptr(q_out), _ptr(kc), _ptr(vc), n, hq,
+                               hkv, max_len, rd, eps, _stream(stream))
+
+
+def decode(q, kc, vc, pos, qg, ldp, part_o, part_ml, out, ldo, n, hq, hkv, max_len, ns,
+           scale=1.0 / 16, stream=None) -> int:
+    return load().qe_attn_decode(_ptr(q), _ptr(kc), _ptr(vc), _ptr(pos), _ptr(qg), ldp,
+                                 _ptr(part_o), _ptr(part_ml), _ptr(out), ldo, n, hq, hkv, max_len,
+                                 ns, scale, _stream(stream))
+
+
+def decode_partials(q, kc, vc, pos, part_o, part_ml, n, hq, hkv, max_len, ns, scale=1.0 / 16,
+                    stream=None) -> int:
+    return load().qe_attn_decode_partials(_ptr(q), _ptr(kc), _ptr(vc), _ptr(pos), _ptr(part_o),
+                                          _ptr(part_ml), n, hq, hkv, max_len, ns, scale,
+                                          _stream(stream))
+
+
+def decode_combine(part_o, part_ml, pos, qg, ldp, out, ldo, n, hq, max_len, ns,
+                   stream=None) -> int:
+    return load().qe_attn_decode_combine(_ptr(part_o), _ptr(part_ml), _ptr(pos), _ptr(qg), ldp,
+                                         _ptr(out), ldo, n, hq, max_len, ns, _stream(stream))
+
+
+def split_size(max_len: int, ns: int) -> int:
+    return load().qe_attn_split_size(max_len, ns)
+
+
+def version() -> str:
+    return load().qe_attn_version().decode()

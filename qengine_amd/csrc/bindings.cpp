@@ -1,0 +1,217 @@
+// torch bindings for qengine_amd._C: the reference's qengine._C attention ops with the same
+// Python signatures and the same validation contract (reference csrc/bindings.cpp:1-30,147-183).
+// Every op writes into caller-provided tensors (no allocation), enqueues on the current HIP stream
+// and never syncs, so it can be captured in a hipGraph. Row-batched arguments are 2-D views
+// [n, width] with stride(1) == 1 and any row stride (a 1-D tensor counts as one row).
+//
+// Each op is a thin shell over the C ABI in include/qe_attn.h. Launch errors are raised as
+// RuntimeError; the reference dropped them (csrc/common.cuh:45).
+//
+// The _check_* functions run the same validation without the device requirement and without a
+// launch, so the contract can be exercised on a machine without a GPU.
+#include <torch/extension.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include "qe_attn.h"
+
+namespace {
+const auto BF = torch::kBFloat16;
+const auto I32 = torch::kInt32;
+const auto F32 = torch::kFloat32;
+constexpr int HD = 256;
+
+hipStream_t stream_of(const torch::Tensor& t) {
+  return c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+
+void chk(const torch::Tensor& t, torch::ScalarType dt, const char* name, bool dev) {
+  if (dev) TORCH_CHECK(t.is_cuda(), name, " must be a GPU tensor");
+  TORCH_CHECK(t.scalar_type() == dt, name, " has wrong dtype ", t.scalar_type());
+  TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+}
+
+// Row view: (rows, width, row stride).
+struct Rows {
+  int n;
+  long w;
+  long ld;
+};
+Rows rows(const torch::Tensor& t, torch::ScalarType dt, const char* name, bool dev) {
+  TORCH_CHECK((!dev || t.is_cuda()) && t.scalar_type() == dt, name, ": wrong device/dtype");
+  if (t.dim() == 1) {
+    TORCH_CHECK(t.stride(0) == 1, name, " not contiguous");
+    return {1, (long)t.size(0), (long)t.size(0)};
+  }
+  TORCH_CHECK(t.dim() == 2 && t.stride(1) == 1, name, " must be [n, w] with unit inner stride");
+  return {(int)t.size(0), (long)t.size(1), (long)t.stride(0)};
+}
+
+void chk16(const torch::Tensor& t, long ld, const char* name) {
+  TORCH_CHECK(reinterpret_cast<uintptr_t>(t.data_ptr()) % 16 == 0 && ld % 8 == 0, name,
+              " must be 16-byte aligned rows");
+}
+
+void chk_pos(const torch::Tensor& pos, bool dev) {
+  TORCH_CHECK((!dev || pos.is_cuda()) && pos.scalar_type() == I32 && pos.numel() >= 1,
+              "pos must be an int32 GPU tensor with at least one element");
+}
+
+void raise_on(hipError_t e, const char* what) {
+  TORCH_CHECK(e == hipSuccess, what, " failed: ", hipGetErrorString(e));
+}
+
+struct PrepArgs {
+  int n, Hq, Hkv, max_len, rd;
+  long ldp;
+};
+
+PrepArgs parse_prep(const torch::Tensor& qg, const torch::Tensor& k, const torch::Tensor& v,
+                    const torch::Tensor& qnw, const torch::Tensor& knw,
+                    const torch::Tensor& inv_freq, const torch::Tensor& pos,
+                    const torch::Tensor& q_out, const torch::Tensor& kc, const torch::Tensor& vc,
+                    bool dev) {
+  auto QG = rows(qg, BF, "qg", dev), K = rows(k, BF, "k", dev), V = rows(v, BF, "v", dev);
+  auto QO = rows(q_out, BF, "q_out", dev);
+  TORCH_CHECK(QG.ld == K.ld && QG.ld == V.ld, "qg/k/v must share a row stride");
+  chk(qnw, BF, "qnw", dev);
+  chk(knw, BF, "knw", dev);
+  chk(kc, BF, "kc", dev);
+  chk(vc, BF, "vc", dev);
+  chk(inv_freq, F32, "inv_freq", dev);
+  chk_pos(pos, dev);
+  TORCH_CHECK(kc.dim() == 3 && kc.size(2) == HD, "head_dim 256 only");
+  const int n = QG.n, Hkv = kc.size(0), max_len = kc.size(1), Hq = QO.w / HD;
+  TORCH_CHECK(n >= 1 && n <= 8 && K.n == n && V.n == n && QO.n == n && QO.ld == QO.w,
+              "prep takes 1..8 rows, equal in every argument, and contiguous q_out rows");
+  TORCH_CHECK(Hq >= 1 && QG.w == (long)Hq * 2 * HD && K.w == (long)Hkv * HD &&
+                  V.w == (long)Hkv * HD,
+              "row widths must be qg = Hq*512, k = v = Hkv*256");
+  TORCH_CHECK(vc.sizes() == kc.sizes() && qnw.numel() == HD && knw.numel() == HD,
+              "vc must match kc; qnw/knw must have 256 elements");
+  const int rd = inv_freq.numel() * 2;
+  TORCH_CHECK(rd <= HD, "rotary dims (2 * inv_freq.numel()) must be <= 256");
+  return {n, Hq, Hkv, max_len, rd, QG.ld};
+}
+
+struct DecodeArgs {
+  int n, Hq, Hkv, max_len, NS;
+  long ldp, ldo;
+};
+
+DecodeArgs parse_decode(const torch::Tensor& q, const torch::Tensor& kc, const torch::Tensor& vc,
+                        const torch::Tensor& pos, const torch::Tensor& qg,
+                        const torch::Tensor& part_o, const torch::Tensor& part_ml,
+                        const torch::Tensor& out, bool dev) {
+  auto Qr = rows(q, BF, "q", dev), QG = rows(qg, BF, "qg", dev), O = rows(out, BF, "out", dev);
+  chk(kc, BF, "kc", dev);
+  chk(vc, BF, "vc", dev);
+  chk(part_o, F32, "part_o", dev);
+  chk(part_ml, F32, "part_ml", dev);
+  chk_pos(pos, dev);
+  chk16(q, Qr.ld, "q");
+  chk16(kc, HD, "kc");
+  chk16(vc, HD, "vc");
+  TORCH_CHECK(kc.dim() == 3 && kc.size(2) == HD && vc.sizes() == kc.sizes(),
+              "kc/vc must be [Hkv, max_len, 256] with equal sizes");
+  const int n = Qr.n, Hq = Qr.w / HD, Hkv = kc.size(0), max_len = kc.size(1);
+  TORCH_CHECK(Hq >= 1 && Qr.ld == Qr.w && QG.n == n && O.n == n && Hq % Hkv == 0,
+              "q rows must be contiguous, rows must agree and Hq % Hkv == 0");
+  TORCH_CHECK(part_o.dim() == 4 && part_o.size(0) >= n && part_o.size(1) == Hq &&
+                  part_o.size(3) == HD,
+              "part_o must be [>=n, Hq, NS, 256]");
+  const int NS = part_o.size(2);
+  TORCH_CHECK(part_ml.numel() == part_o.size(0) * Hq * NS * 2 && O.w == (long)Hq * HD &&
+                  QG.w == (long)Hq * 2 * HD,
+              "part_ml must be [>=n, Hq, NS, 2]; out width Hq*256; qg width Hq*512");
+  TORCH_CHECK(n >= 1 && n <= 8, "decode takes 1..8 rows");
+  TORCH_CHECK((Hq / Hkv) * n <= 64, "GQA group size * rows must be <= 64");
+  TORCH_CHECK(NS >= 1, "part_o needs at least one split");
+  return {n, Hq, Hkv, max_len, NS, QG.ld, O.ld};
+}
+}  // namespace
+
+// pos: int32 tensor whose element 0 is the position of row 0.
+void attn_prep(torch::Tensor qg, torch::Tensor k, torch::Tensor v, torch::Tensor qnw,
+               torch::Tensor knw, torch::Tensor inv_freq, torch::Tensor pos, torch::Tensor q_out,
+               torch::Tensor kc, torch::Tensor vc, double eps) {
+  const auto a = parse_prep(qg, k, v, qnw, knw, inv_freq, pos, q_out, kc, vc, true);
+  const c10::DeviceGuard guard(qg.device());
+  raise_on(qe_attn_prep(qg.data_ptr(), k.data_ptr(), v.data_ptr(), a.ldp, qnw.data_ptr(),
+                        knw.data_ptr(), inv_freq.data_ptr<float>(), pos.data_ptr<int>(),
+                        q_out.data_ptr(), kc.data_ptr(), vc.data_ptr(), a.n, a.Hq, a.Hkv,
+                        a.max_len, a.rd, (float)eps, stream_of(qg)),
+           "qe_attn_prep");
+}
+
+// q: [n, Hq*256] contiguous; part_o: fp32 [>=n, Hq, NS, 256]; part_ml: [>=n, Hq, NS, 2];
+// out: [n, Hq*256] gated by sigmoid of the gate half of the qg rows.
+void attn_decode(torch::Tensor q, torch::Tensor kc, torch::Tensor vc, torch::Tensor pos,
+                 torch::Tensor qg, torch::Tensor part_o, torch::Tensor part_ml, torch::Tensor out) {
+  const auto a = parse_decode(q, kc, vc, pos, qg, part_o, part_ml, out, true);
+  const c10::DeviceGuard guard(q.device());
+  raise_on(qe_attn_decode(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), pos.data_ptr<int>(),
+                          qg.data_ptr(), a.ldp, part_o.data_ptr<float>(),
+                          part_ml.data_ptr<float>(), out.data_ptr(), a.ldo, a.n, a.Hq, a.Hkv,
+                          a.max_len, a.NS, 1.0f / 16.0f /* 256^-0.5 */, stream_of(q)),
+           "qe_attn_decode");
+}
+
+// The two halves of attn_decode (same arguments): split-KV partials, then the gated combine.
+void attn_decode_partials(torch::Tensor q, torch::Tensor kc, torch::Tensor vc, torch::Tensor pos,
+                          torch::Tensor qg, torch::Tensor part_o, torch::Tensor part_ml,
+                          torch::Tensor out) {
+  const auto a = parse_decode(q, kc, vc, pos, qg, part_o, part_ml, out, true);
+  const c10::DeviceGuard guard(q.device());
+  raise_on(qe_attn_decode_partials(q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                   pos.data_ptr<int>(), part_o.data_ptr<float>(),
+                                   part_ml.data_ptr<float>(), a.n, a.Hq, a.Hkv, a.max_len, a.NS,
+                                   1.0f / 16.0f, stream_of(q)),
+           "qe_attn_decode_partials");
+}
+
+void attn_decode_combine(torch::Tensor q, torch::Tensor kc, torch::Tensor vc, torch::Tensor pos,
+                         torch::Tensor qg, torch::Tensor part_o, torch::Tensor part_ml,
+                         torch::Tensor out) {
+  const auto a = parse_decode(q, kc, vc, pos, qg, part_o, part_ml, out, true);
+  const c10::DeviceGuard guard(q.device());
+  raise_on(qe_attn_decode_combine(part_o.data_ptr<float>(), part_ml.data_ptr<float>(),
+                                  pos.data_ptr<int>(), qg.data_ptr(), a.ldp, out.data_ptr(),
+                                  a.ldo, a.n, a.Hq, a.max_len, a.NS, stream_of(q)),
+           "qe_attn_decode_combine");
+}
+
+std::vector<int64_t> check_attn_prep(torch::Tensor qg, torch::Tensor k, torch::Tensor v,
+                                     torch::Tensor qnw, torch::Tensor knw, torch::Tensor inv_freq,
+                                     torch::Tensor pos, torch::Tensor q_out, torch::Tensor kc,
+                                     torch::Tensor vc) {
+  const auto a = parse_prep(qg, k, v, qnw, knw, inv_freq, pos, q_out, kc, vc, false);
+  return {a.n, a.Hq, a.Hkv, a.max_len, a.rd, a.ldp};
+}
+
+std::vector<int64_t> check_attn_decode(torch::Tensor q, torch::Tensor kc, torch::Tensor vc,
+                                       torch::Tensor pos, torch::Tensor qg, torch::Tensor part_o,
+                                       torch::Tensor part_ml, torch::Tensor out) {
+  const auto a = parse_decode(q, kc, vc, pos, qg, part_o, part_ml, out, false);
+  return {a.n, a.Hq, a.Hkv, a.max_len, a.NS, a.ldp, a.ldo};
+}
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.doc() = "MI355X (gfx950) gated-attention decode ops with qengine._C's signatures";
+  m.def("attn_prep", &attn_prep);
+  m.def("attn_decode", &attn_decode);
+  m.def("attn_decode_partials", &attn_decode_partials,
+        "split-KV partials of attn_decode (same arguments)");
+  m.def("attn_decode_combine", &attn_decode_combine,
+        "log-sum-exp combine + sigmoid gate of attn_decode (same arguments)");
+  m.def("split_size", [](int max_len, int NS) { return qe_attn_split_size(max_len, NS); },
+        "cache positions per split-KV slice for (max_len, NS)");
+  m.def("version", []() { return std::string(qe_attn_version()); });
+  m.def("set_pdl_trigger", [](bool on) { qe_set_pdl_trigger(on); },
+        "no-op on gfx950 (kept for import compatibility)");
+  m.def("set_pdl_launch", [](bool on) { qe_set_pdl_launch(on); },
+        "no-op on gfx950 (kept for import compatibility)");
+  m.def("_check_attn_prep", &check_attn_prep, "validate attn_prep arguments without launching");
+  m.def("_check_attn_decode", &check_attn_decode,
+        "validate attn_decode arguments without launching");
+}

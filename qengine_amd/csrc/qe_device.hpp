@@ -1,0 +1,78 @@
+// Device helpers shared by the gfx950 attention kernels: bf16 rounding, wave64 reductions,
+// buffer-resource loads and the MFMA operand types.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qe {
+
+constexpr int HD = 256;      // head_dim (fixed, as in the reference: csrc/attn.cu:15)
+constexpr int WAVE = 64;     // CDNA wavefront
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------- bf16 rounding
+// torch rounds every bf16 op result to nearest-even; these model one such rounding.
+__device__ __forceinline__ float bf16_to_f32(__bf16 x) { return static_cast<float>(x); }
+__device__ __forceinline__ __bf16 f32_to_bf16(float x) { return static_cast<__bf16>(x); }
+__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+// The high/low bf16 of a packed dword as fp32 (exact).
+__device__ __forceinline__ float lo_bf16(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float hi_bf16(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+
+// Pack two fp32 into a dword of two bf16 (round to nearest even): a -> low half, b -> high.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const uint32_t lo = __builtin_bit_cast(uint16_t, f32_to_bf16(a));
+  const uint32_t hi = __builtin_bit_cast(uint16_t, f32_to_bf16(b));
+  return lo | (hi << 16);
+}
+
+// dword made of the low halves (sel_hi = false) or high halves (true) of x (-> low) and y (-> high)
+__device__ __forceinline__ uint32_t interleave_halves(uint32_t x, uint32_t y, bool sel_hi) {
+  return __builtin_amdgcn_perm(y, x, sel_hi ? 0x07060302u : 0x05040100u);
+}
+
+// sigmoid in fp32, as torch.sigmoid evaluates a bf16 input before rounding the result.
+__device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// ---------------------------------------------------------------------------- reductions
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Max / sum across the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48).
+__device__ __forceinline__ float group4_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  return fmaxf(v, __shfl_xor(v, 32));
+}
+__device__ __forceinline__ float group4_sum(float v) {
+  v += __shfl_xor(v, 16);
+  return v + __shfl_xor(v, 32);
+}
+
+// ---------------------------------------------------------------------------- buffer loads
+// Raw buffer resource over [base, base + bytes). Loads whose dword lies past `bytes` return 0
+// (no fault), which the kernels use to zero-fill positions beyond the attended range.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ u32x4_t buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(u32x4_t,
+                            __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0));
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// D = A(16x32) * B(32x16) + C on bf16 inputs with fp32 accumulation. Lane l holds A row l%16 /
+// B column l%16 at k = 8*(l/16)+e, and D rows 4*(l/16)+i of column l%16.
+__device__ __forceinline__ f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace qe

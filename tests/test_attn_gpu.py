@@ -1,0 +1,335 @@
+"""GPU parity tests: the gfx950 kernels vs the CPU oracle on identical seeded inputs.
+
+Bars:
+  prep   : q and k within 1 bf16 ulp of the oracle, v copied exactly (reference
+           tests/test_kernels.py:341-346).
+  decode : per element |out-ref| <= 2^-6|ref| + 2e-3 (reference tests/test_kernels.py:353) and
+           max-abs <= 2e-2, mean-abs <= 2e-3 (BASELINE gate), fp32 accumulation.
+  rows   : row t of an n-row call is bit-identical to a 1-row call at position pos+t
+           (reference tests/test_kernels.py:354-357); MTP verify argmax == sequential decodes.
+"""
+import pytest
+import torch
+
+import oracle as O
+from attn_cases import BF, D, attn_close, decode_case, gen, norm_weights, proj_rows, ulp_close
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _dev(t):
+    return t.to(DEV)
+
+
+def gpu_decode(C, case, ns, pos=None, rows=None):
+    """Run attn_decode on the GPU for `case` (optionally a row slice / other pos)."""
+    q, qg = case.q, case.qg
+    if rows is not None:
+        q, qg = q[rows], qg[rows]
+    n = q.shape[0]
+    p = case.pos if pos is None else pos
+    out = torch.empty(n, case.hq * D, dtype=BF, device=DEV)
+    po = torch.empty(n, case.hq, ns, D, device=DEV)
+    pml = torch.empty(n, case.hq, ns, 2, device=DEV)
+    kc, vc = getattr(case, "_kc_dev", None), getattr(case, "_vc_dev", None)
+    if kc is None:
+        kc, vc = _dev(case.kc), _dev(case.vc)
+        case._kc_dev, case._vc_dev = kc, vc
+    C.attn_decode(_dev(q), kc, vc, torch.tensor([p], dtype=torch.int32, device=DEV), _dev(qg),
+                  po, pml, out)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def oracle_decode(case):
+    return O.attn_decode(case.q, case.kc, case.vc, case.pos, case.qg, case.hq)
+
+
+# ------------------------------------------------------------------ reference unit-test cases
+@pytest.mark.parametrize("hq,hkv,steps,start,n", [(8, 2, 20, 0, 1), (24, 4, 6, 0, 1),
+                                                    (8, 2, 3, 4094, 1), (1, 1, 5, 125, 1),
+                                                    (8, 2, 24, 0, 8), (24, 4, 12, 100, 3)])
+def test_attention_reference_cases(native, hq, hkv, steps, start, n):
+    """The reference's test_attention (tests/test_kernels.py:302-357) on the oracle: passes of n
+    rows at start, start+n, ...; prep vs oracle (q/k <= 1 ulp, v exact); decode on the oracle's
+    cache vs oracle attention; each row bit-identical to a 1-row pass."""
+    C = native
+    g = gen(1)
+    max_len = start + steps
+    qnw, knw = norm_weights(g)
+    kc = torch.zeros(hkv, max_len, D, dtype=BF)
+    vc = torch.zeros_like(kc)
+    kc[:, :start] = torch.randn(hkv, start, D, generator=g).to(BF)
+    vc[:, :start] = torch.randn(hkv, start, D, generator=g).to(BF)
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    kc_d, vc_d = _dev(kc), _dev(vc)
+    inv = O.rope_inv_freq(1e7, 64)
+    NS = 16
+    po = torch.empty(8, hq, NS, D, device=DEV)
+    pml = torch.empty(8, hq, NS, 2, device=DEV)
+    pos_t = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for p0 in range(start, start + steps, n):
+        nn = min(n, start + steps - p0)
+        pr = proj_rows(g, nn, hq, hkv)
+        q_ref = O.attn_prep(pr.qg, pr.k, pr.v, qnw, knw, inv, p0, kc_ref, vc_ref, 1e-6, hq)
+        refs = O.attn_decode(q_ref, kc_ref, vc_ref, p0, pr.qg, hq)
+        pos_t.fill_(p0)
+        prd = _dev(pr.proj)
+        qg_d = prd[:, : hq * 2 * D]
+        k_d = prd[:, hq * 2 * D: hq * 2 * D + hkv * D]
+        v_d = prd[:, hq * 2 * D + hkv * D: hq * 2 * D + 2 * hkv * D]
+        q_out = torch.empty(nn, hq * D, dtype=BF, device=DEV)
+        C.attn_prep(qg_d, k_d, v_d, _dev(qnw), _dev(knw), _dev(inv), pos_t, q_out, kc_d, vc_d, 1e-6)
+        ok, err = ulp_close(q_out.cpu(), q_ref, ulps=1)
+        assert ok, ("q", p0, err)
+        ok, err = ulp_close(kc_d[:, p0:p0 + nn].cpu(), kc_ref[:, p0:p0 + nn], ulps=1)
+        assert ok, ("k", p0, err)
+        assert torch.equal(vc_d[:, p0:p0 + nn].cpu(), vc_ref[:, p0:p0 + nn])
+        # attention on the oracle's cache so the check is independent of q/k rounding flips
+        kr, vr, qr = _dev(kc_ref), _dev(vc_ref), _dev(q_ref)
+        out = torch.empty(nn, hq * D, dtype=BF, device=DEV)
+        C.attn_decode(qr, kr, vr, pos_t, qg_d, po, pml, out)
+        for t in range(nn):
+            ok, mx, mean = attn_close(out[t].cpu(), refs[t])
+            assert ok, (p0 + t, mx, mean)
+            o1 = torch.empty(1, hq * D, dtype=BF, device=DEV)
+            C.attn_decode(qr[t:t + 1], kr, vr, pos_t + t, qg_d[t:t + 1], po, pml, o1)
+            assert torch.equal(o1[0], out[t]), ("row bit-exactness", p0 + t)
+
+
+# ------------------------------------------------------------------ BASELINE configurations
+def test_config1_prep_and_decode(native):
+    """cfg 1: one layer, one decode step at KV 1024 (pos 1023), 24 Q / 4 KV heads, theta 1e7,
+    rotary 64, scale 1/16: full prep (writes position 1023) + decode."""
+    C = native
+    hq, hkv, L = 24, 4, 1024
+    g = gen(0)
+    kc = torch.zeros(hkv, L, D, dtype=BF)
+    vc = torch.zeros_like(kc)
+    kc[:, :L - 1] = torch.randn(hkv, L - 1, D, generator=g).to(BF)
+    vc[:, :L - 1] = torch.randn(hkv, L - 1, D, generator=g).to(BF)
+    qnw, knw = norm_weights(g)
+    pr = proj_rows(g, 1, hq, hkv)
+    inv = O.rope_inv_freq(1e7, 64)
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    q_ref = O.attn_prep(pr.qg, pr.k, pr.v, qnw, knw, inv, L - 1, kc_ref, vc_ref, 1e-6, hq)
+    ref = O.attn_decode(q_ref, kc_ref, vc_ref, L - 1, pr.qg, hq)
+    kc_d, vc_d, prd = _dev(kc), _dev(vc), _dev(pr.proj)
+    qg_d = prd[:, : hq * 2 * D]
+    k_d = prd[:, hq * 2 * D: hq * 2 * D + hkv * D]
+    v_d = prd[:, hq * 2 * D + hkv * D: hq * 2 * D + 2 * hkv * D]
+    pos = torch.tensor([L - 1], dtype=torch.int32, device=DEV)
+    q = torch.empty(1, hq * D, dtype=BF, device=DEV)
+    C.attn_prep(qg_d, k_d, v_d, _dev(qnw), _dev(knw), _dev(inv), pos, q, kc_d, vc_d, 1e-6)
+    NS = 16
+    po = torch.empty(1, hq, NS, D, device=DEV)
+    pml = torch.empty(1, hq, NS, 2, device=DEV)
+    out = torch.empty(1, hq * D, dtype=BF, device=DEV)
+    C.attn_decode(q, kc_d, vc_d, pos, qg_d, po, pml, out)
+    ok, mx, mean = attn_close(out.cpu(), ref)
+    assert ok, (mx, mean)
+
+
+@pytest.mark.parametrize("L", [1024, 4096, 16384, 32768])
+@pytest.mark.parametrize("ns", [16, 64])
+def test_config2_split_sweep(native, L, ns):
+    """cfg 2: split-KV decode at KV 4k/16k/32k (and cfg 1's 1k), N(0,1) cache, seeded."""
+    case = decode_case(seed=L, hq=24, hkv=4, pos=L - 1, n=1)
+    out = gpu_decode(native, case, ns)
+    ok, mx, mean = attn_close(out, oracle_decode(case))
+    assert ok, (L, ns, mx, mean)
+
+
+@pytest.mark.parametrize("adversarial", [False, True])
+def test_config4_long_context(native, adversarial):
+    """cfg 4: KV 131072 (537 MB of K+V); the adversarial variant scales 1% of key rows by 8."""
+    L = 131072
+    case = decode_case(seed=4, hq=24, hkv=4, pos=L - 1, n=1,
+                       key_scale_frac=0.01 if adversarial else 0.0)
+    out = gpu_decode(native, case, 512)
+    ok, mx, mean = attn_close(out, oracle_decode(case))
+    assert ok, (adversarial, mx, mean)
+
+
+def test_config3_mtp_verify(native):
+    """cfg 3: 5 rows (1 accepted + 4 drafts) at pos 4096, causal among themselves, over 4096
+    cached + 5 new rows. Rows must be bit-identical to 5 sequential 1-row decodes, so argmax over a
+    seeded bf16 projection [151936 x 5120] . [5120 x 6144] of the outputs is identical; both
+    also stay within tolerance of the oracle."""
+    C = native
+    case = decode_case(seed=3, hq=24, hkv=4, pos=4096, n=5, max_len=4096 + 64)
+    ns = 16
+    verify = gpu_decode(C, case, ns)
+    seq = torch.cat([gpu_decode(C, case, ns, pos=case.pos + t, rows=slice(t, t + 1))
+                     for t in range(5)])
+    assert torch.equal(verify, seq)
+    ref = oracle_decode(case)
+    ok, mx, mean = attn_close(verify, ref)
+    assert ok, (mx, mean)
+    gd = torch.Generator(device=DEV).manual_seed(33)
+    w_o = (torch.randn(5120, 24 * D, generator=gd, device=DEV) * (24 * D) ** -0.5).to(BF)
+    w_lm = (torch.randn(151936, 5120, generator=gd, device=DEV) * 5120 ** -0.5).to(BF)
+
+    def tokens(o):
+        h = o.to(DEV) @ w_o.t()
+        return (h @ w_lm.t()).float().argmax(-1).cpu()
+
+    assert torch.equal(tokens(verify), tokens(seq))
+    agree = (tokens(verify) == tokens(ref)).float().mean().item()
+    assert agree >= 0.8, agree  # vs the oracle: same argmax unless two logits nearly tie
+
+
+# ------------------------------------------------------------------ semantics and edge cases
+@pytest.mark.parametrize("ns", [1, 3, 16, 100, 1000])
+def test_split_count_does_not_matter(native, ns):
+    """Any split count gives the oracle's answer (slices of split_size(max_len, NS) positions)."""
+    case = decode_case(seed=7, hq=24, hkv=4, pos=3000, n=3, max_len=5000)
+    ok, mx, mean = attn_close(gpu_decode(native, case, ns), oracle_decode(case))
+    assert ok, (ns, mx, mean)
+
+
+@pytest.mark.parametrize("hq,hkv,n", [(24, 4, 8), (8, 2, 8), (8, 1, 8), (16, 1, 4), (4, 4, 2),
+                                      (32, 8, 7), (6, 1, 1)])
+def test_gqa_shapes_and_rows(native, hq, hkv, n):
+    """Group sizes 1..16 and 1..8 rows (1 to 4 MFMA column tiles) vs the oracle, rows bit-exact."""
+    case = decode_case(seed=hq * 10 + n, hq=hq, hkv=hkv, pos=777, n=n, max_len=1000)
+    out = gpu_decode(native, case, 8)
+    ok, mx, mean = attn_close(out, oracle_decode(case))
+    assert ok, (mx, mean)
+    for t in range(n):
+        o1 = gpu_decode(native, case, 8, pos=case.pos + t, rows=slice(t, t + 1))
+        assert torch.equal(o1[0], out[t]), t
+
+
+def test_max_len_clamp(native):
+    """Rows past the end of the cache attend the whole cache (attn.cu:78)."""
+    case = decode_case(seed=11, hq=24, hkv=4, pos=1000, n=6, max_len=1003)
+    ok, mx, mean = attn_close(gpu_decode(native, case, 4), oracle_decode(case))
+    assert ok, (mx, mean)
+
+
+@pytest.mark.parametrize("pos", [0, 1, 31, 32, 33, 255, 256, 257])
+def test_short_prefixes(native, pos):
+    """Tile and slice boundaries at short lengths, including a single attended position."""
+    case = decode_case(seed=pos, hq=24, hkv=4, pos=pos, n=2, max_len=300)
+    ok, mx, mean = attn_close(gpu_decode(native, case, 4), oracle_decode(case))
+    assert ok, (pos, mx, mean)
+
+
+def test_unattended_cache_is_never_read(native):
+    """NaN in cache rows past the attended range must not reach the output."""
+    clean = decode_case(seed=5, hq=24, hkv=4, pos=500, n=4, max_len=700)
+    dirty = decode_case(seed=5, hq=24, hkv=4, pos=500, n=4, max_len=700)
+    dirty.kc[:, 504:] = float("nan")
+    dirty.vc[:, 504:] = float("nan")
+    a, b = gpu_decode(native, clean, 16), gpu_decode(native, dirty, 16)
+    assert torch.isfinite(b.float()).all()
+    assert torch.equal(a, b)
+
+
+def test_partials_then_combine_equals_decode(native):
+    """attn_decode == attn_decode_partials followed by attn_decode_combine, bit for bit."""
+    C = native
+    case = decode_case(seed=9, hq=24, hkv=4, pos=9000, n=2, max_len=9100)
+    ns = 40
+    ref = gpu_decode(C, case, ns)
+    q, qg, kc, vc = _dev(case.q), _dev(case.qg), _dev(case.kc), _dev(case.vc)
+    pos = torch.tensor([case.pos], dtype=torch.int32, device=DEV)
+    po = torch.empty(2, 24, ns, D, device=DEV)
+    pml = torch.empty(2, 24, ns, 2, device=DEV)
+    out = torch.empty(2, 24 * D, dtype=BF, device=DEV)
+    C.attn_decode_partials(q, kc, vc, pos, qg, po, pml, out)
+    C.attn_decode_combine(q, kc, vc, pos, qg, po, pml, out)
+    assert torch.equal(out.cpu(), ref)
+
+
+# ------------------------------------------------------------------ C ABI and graph capture
+def test_capi_matches_extension(native, capi):
+    """The C ABI (ctypes, no torch extension) gives the extension's bits for prep and decode."""
+    C = native
+    hq, hkv, max_len, n = 24, 4, 2048, 3
+    g = gen(21)
+    qnw, knw = norm_weights(g)
+    pr = proj_rows(g, n, hq, hkv)
+    inv = _dev(O.rope_inv_freq(1e7, 64))
+    base = decode_case(seed=21, hq=hq, hkv=hkv, pos=1500, n=n, max_len=max_len)
+    outs = []
+    for path in ("ext", "capi"):
+        kc, vc = _dev(base.kc), _dev(base.vc)
+        prd = _dev(pr.proj)
+        ldp = prd.stride(0)
+        qg_d = prd[:, : hq * 2 * D]
+        k_d = prd[:, hq * 2 * D: hq * 2 * D + hkv * D]
+        v_d = prd[:, hq * 2 * D + hkv * D: hq * 2 * D + 2 * hkv * D]
+        pos = torch.tensor([base.pos], dtype=torch.int32, device=DEV)
+        q = torch.empty(n, hq * D, dtype=BF, device=DEV)
+        ns = 8
+        po = torch.empty(n, hq, ns, D, device=DEV)
+        pml = torch.empty(n, hq, ns, 2, device=DEV)
+        out = torch.empty(n, hq * D, dtype=BF, device=DEV)
+        qn, kn = _dev(qnw), _dev(knw)
+        if path == "ext":
+            C.attn_prep(qg_d, k_d, v_d, qn, kn, inv, pos, q, kc, vc, 1e-6)
+            C.attn_decode(q, kc, vc, pos, qg_d, po, pml, out)
+        else:
+            assert capi.prep(qg_d, k_d, v_d, ldp, qn, kn, inv, pos, q, kc, vc, n, hq, hkv,
+                             max_len, 64, 1e-6) == 0
+            assert capi.decode(q, kc, vc, pos, qg_d, ldp, po, pml, out, hq * D, n, hq, hkv,
+                               max_len, ns) == 0
+        torch.cuda.synchronize()
+        outs.append((q.cpu(), kc.cpu(), vc.cpu(), out.cpu()))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+def test_graph_capture_replays(native):
+    """prep + decode captured in one hipGraph, replayed at advancing positions with eager work
+    in between; every replay equals the eager result (pos is read on the device)."""
+    C = native
+    hq, hkv, max_len, n = 24, 4, 4096, 1
+    g = gen(31)
+    qnw, knw = _dev(norm_weights(g)[0]), _dev(norm_weights(g)[1])
+    inv = _dev(O.rope_inv_freq(1e7, 64))
+    base = decode_case(seed=31, hq=hq, hkv=hkv, pos=2000, n=n, max_len=max_len)
+    pr = proj_rows(g, n, hq, hkv)
+    prd = _dev(pr.proj)
+    qg_d = prd[:, : hq * 2 * D]
+    k_d = prd[:, hq * 2 * D: hq * 2 * D + hkv * D]
+    v_d = prd[:, hq * 2 * D + hkv * D: hq * 2 * D + 2 * hkv * D]
+    ns = 16
+    po = torch.empty(n, hq, ns, D, device=DEV)
+    pml = torch.empty(n, hq, ns, 2, device=DEV)
+
+    def make_state():
+        return (_dev(base.kc), _dev(base.vc), torch.empty(n, hq * D, dtype=BF, device=DEV),
+                torch.empty(n, hq * D, dtype=BF, device=DEV),
+                torch.tensor([base.pos], dtype=torch.int32, device=DEV))
+
+    def step(st):
+        kc, vc, q, out, pos = st
+        C.attn_prep(qg_d, k_d, v_d, qnw, knw, inv, pos, q, kc, vc, 1e-6)
+        C.attn_decode(q, kc, vc, pos, qg_d, po, pml, out)
+
+    eager, graphed = make_state(), make_state()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step(graphed)  # warm-up outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    graphed[4].fill_(base.pos)
+    graphed[0].copy_(_dev(base.kc))
+    graphed[1].copy_(_dev(base.vc))
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step(graphed)
+    for r in range(4):
+        step(eager)
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(eager[:4], graphed[:4]):
+            assert torch.equal(a, b), r
+        eager[4].add_(1)
+        graphed[4].add_(1)
+        torch.cuda.synchronize()

@@ -1,0 +1,200 @@
+"""CPU tests of the drop-in boundary: the C-ABI library loads and exports every entry point that
+include/qe_attn.h declares, the C ABI rejects out-of-range arguments before launching anything,
+and the torch extension enforces the reference's validation contract
+(reference csrc/bindings.cpp:15-30,147-183). No kernel runs here."""
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "qe_attn.h"
+BF, F32, I32 = torch.bfloat16, torch.float32, torch.int32
+D = 256
+INVALID = 1  # hipErrorInvalidValue
+
+
+def declared_symbols():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(qe_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_path():
+    syms = declared_symbols()
+    for s in ("qe_attn_prep", "qe_attn_decode", "qe_attn_decode_partials",
+              "qe_attn_decode_combine", "qe_attn_split_size", "qe_attn_version"):
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol(capi):
+    lib = capi.load()
+    for s in declared_symbols():
+        assert hasattr(lib, s), s
+    assert set(capi.SIGNATURES) == set(declared_symbols())
+
+
+def test_version_and_split_size(capi):
+    assert "gfx950" in capi.version()
+    assert capi.split_size(4096, 16) == 256          # the reference engine's defaults
+    assert capi.split_size(16384, 64) == 256
+    assert capi.split_size(1000, 3) == 352           # ceil(1000/3) = 334 -> multiple of 32
+    assert capi.split_size(10, 100) == 32            # never below one 32-position tile
+    assert capi.split_size(0, 4) == 0 and capi.split_size(8, 0) == 0
+    for max_len in (1, 31, 32, 33, 4097, 131072):
+        for ns in (1, 7, 16, 512):
+            ch = capi.split_size(max_len, ns)
+            assert ch % 32 == 0 and ch * ns >= max_len
+
+
+# Fake 16-byte aligned addresses: the C ABI validates before touching them.
+A = 1 << 20
+
+
+@pytest.mark.parametrize("kw,why", [
+    (dict(n=0), "no rows"), (dict(n=9), "more than 8 rows"), (dict(hq=25), "Hq % Hkv"),
+    (dict(hq=68, hkv=1, n=1), "group*n > 64"), (dict(hq=24, n=3, hkv=1), "group*n > 64"),
+    (dict(ns=0), "no splits"), (dict(max_len=0), "empty cache"),
+    (dict(max_len=1 << 23), "cache beyond 32-bit buffer offsets"),
+    (dict(q=A + 8), "unaligned q"), (dict(kc=A + 2), "unaligned kc"),
+])
+def test_capi_decode_rejects(capi, kw, why):
+    a = dict(q=A, kc=A, vc=A, pos=A, qg=A, ldp=24 * 512, part_o=A, part_ml=A, out=A,
+             ldo=24 * D, n=1, hq=24, hkv=4, max_len=4096, ns=16)
+    a.update(kw)
+    r = capi.load().qe_attn_decode(a["q"], a["kc"], a["vc"], a["pos"], a["qg"], a["ldp"],
+                                   a["part_o"], a["part_ml"], a["out"], a["ldo"], a["n"], a["hq"],
+                                   a["hkv"], a["max_len"], a["ns"], 1.0 / 16, None)
+    assert r == INVALID, why
+
+
+@pytest.mark.parametrize("kw,why", [
+    (dict(n=0), "no rows"), (dict(rd=3), "odd rotary dims"), (dict(rd=258), "rd > 256"),
+    (dict(max_len=0), "empty cache"), (dict(hkv=0), "no kv heads"), (dict(qg=None), "null"),
+])
+def test_capi_prep_rejects(capi, kw, why):
+    a = dict(qg=A, k=A, v=A, ldp=8, qnw=A, knw=A, inv=A, pos=A, q_out=A, kc=A, vc=A, n=1, hq=24,
+             hkv=4, max_len=4096, rd=64)
+    a.update(kw)
+    r = capi.load().qe_attn_prep(a["qg"], a["k"], a["v"], a["ldp"], a["qnw"], a["knw"], a["inv"],
+                                 a["pos"], a["q_out"], a["kc"], a["vc"], a["n"], a["hq"], a["hkv"],
+                                 a["max_len"], a["rd"], 1e-6, None)
+    assert r == INVALID, why
+
+
+def test_pdl_switches_are_noops(native):
+    native.set_pdl_trigger(True)
+    native.set_pdl_launch(False)
+
+
+# ------------------------------------------------------------------ torch-level contract (CPU)
+def decode_args(n=2, hq=24, hkv=4, max_len=64, ns=4, ldp_pad=8):
+    q = torch.zeros(n, hq * D, dtype=BF)
+    kc = torch.zeros(hkv, max_len, D, dtype=BF)
+    vc = torch.zeros_like(kc)
+    pos = torch.zeros(1, dtype=I32)
+    qg = torch.zeros(n, hq * 2 * D + ldp_pad, dtype=BF)[:, : hq * 2 * D]
+    po = torch.zeros(max(8, n), hq, ns, D, dtype=F32)
+    pml = torch.zeros(max(8, n), hq, ns, 2, dtype=F32)
+    out = torch.zeros(n, hq * D, dtype=BF)
+    return dict(q=q, kc=kc, vc=vc, pos=pos, qg=qg, part_o=po, part_ml=pml, out=out)
+
+
+def check_decode(C, a):
+    return C._check_attn_decode(a["q"], a["kc"], a["vc"], a["pos"], a["qg"], a["part_o"],
+                                a["part_ml"], a["out"])
+
+
+def test_decode_contract_accepts_engine_layout(native):
+    n, hq, hkv, max_len, ns, ldp, ldo = check_decode(native, decode_args())
+    assert (n, hq, hkv, max_len, ns) == (2, 24, 4, 64, 4)
+    assert ldp == 24 * 2 * D + 8 and ldo == 24 * D
+    one_row = decode_args(n=1)
+    one_row["q"], one_row["out"] = one_row["q"][0], one_row["out"][0]   # 1-D counts as one row
+    one_row["qg"] = one_row["qg"][0]
+    assert check_decode(native, one_row)[0] == 1
+
+
+def _mut(**changes):
+    def f(a):
+        a.update({k: v(a) for k, v in changes.items()})
+        return a
+    return f
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (_mut(q=lambda a: a["q"].float()), "wrong device/dtype"),
+    (_mut(kc=lambda a: a["kc"].float()), "wrong dtype"),
+    (_mut(part_o=lambda a: a["part_o"].to(BF)), "wrong dtype"),
+    (_mut(pos=lambda a: a["pos"].long()), "int32"),
+    (_mut(kc=lambda a: a["kc"].transpose(0, 1)), "contiguous"),
+    (_mut(q=lambda a: torch.zeros(2, 24 * D + 8, dtype=BF)[:, : 24 * D]), "contiguous"),
+    (_mut(out=lambda a: torch.zeros(3, 24 * D, dtype=BF)), "rows must agree"),
+    (_mut(kc=lambda a: torch.zeros(5, 64, D, dtype=BF), vc=lambda a: torch.zeros(5, 64, D, dtype=BF)),
+     "Hq % Hkv"),
+    (_mut(part_o=lambda a: torch.zeros(1, 24, 4, D)), "part_o"),
+    (_mut(part_o=lambda a: torch.zeros(8, 24, 4, 128)), "part_o"),
+    (_mut(part_ml=lambda a: torch.zeros(8, 24, 3, 2)), "part_ml"),
+    (_mut(qg=lambda a: torch.zeros(2, 24 * D, dtype=BF)), "qg width"),
+    (_mut(vc=lambda a: torch.zeros(4, 32, D, dtype=BF)), "equal sizes"),
+    (_mut(kc=lambda a: torch.zeros(4, 64, 128, dtype=BF), vc=lambda a: torch.zeros(4, 64, 128, dtype=BF)),
+     "256"),
+])
+def test_decode_contract_rejects(native, mutate, msg):
+    a = mutate(decode_args())
+    with pytest.raises(RuntimeError, match=msg):
+        check_decode(native, a)
+
+
+def test_decode_contract_row_limits(native):
+    with pytest.raises(RuntimeError, match="1..8 rows"):
+        check_decode(native, decode_args(n=9))
+    with pytest.raises(RuntimeError, match="<= 64"):
+        check_decode(native, decode_args(n=8, hq=32, hkv=2))   # 16 * 8 = 128 columns
+
+
+def test_decode_requires_gpu_tensors(native):
+    a = decode_args()
+    with pytest.raises(RuntimeError, match="device"):
+        native.attn_decode(a["q"], a["kc"], a["vc"], a["pos"], a["qg"], a["part_o"], a["part_ml"],
+                           a["out"])
+
+
+def prep_args(n=2, hq=24, hkv=4, max_len=64, rd=64, pad=8):
+    w = hq * 2 * D + 2 * hkv * D
+    proj = torch.zeros(n, w + pad, dtype=BF)
+    return dict(qg=proj[:, : hq * 2 * D], k=proj[:, hq * 2 * D: hq * 2 * D + hkv * D],
+                v=proj[:, hq * 2 * D + hkv * D: w], qnw=torch.zeros(D, dtype=BF),
+                knw=torch.zeros(D, dtype=BF), inv_freq=torch.zeros(rd // 2, dtype=F32),
+                pos=torch.zeros(1, dtype=I32), q_out=torch.zeros(n, hq * D, dtype=BF),
+                kc=torch.zeros(hkv, max_len, D, dtype=BF), vc=torch.zeros(hkv, max_len, D, dtype=BF))
+
+
+def check_prep(C, a):
+    return C._check_attn_prep(a["qg"], a["k"], a["v"], a["qnw"], a["knw"], a["inv_freq"],
+                              a["pos"], a["q_out"], a["kc"], a["vc"])
+
+
+def test_prep_contract_accepts_engine_layout(native):
+    n, hq, hkv, max_len, rd, ldp = check_prep(native, prep_args())
+    assert (n, hq, hkv, max_len, rd) == (2, 24, 4, 64, 64)
+    assert ldp == 24 * 2 * D + 2 * 4 * D + 8
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (_mut(k=lambda a: torch.zeros(2, 4 * D, dtype=BF)), "share a row stride"),
+    (_mut(inv_freq=lambda a: torch.zeros(32, dtype=BF)), "wrong dtype"),
+    (_mut(qnw=lambda a: torch.zeros(128, dtype=BF)), "256 elements"),
+    (_mut(kc=lambda a: torch.zeros(4, 64, 128, dtype=BF)), "head_dim 256"),
+    (_mut(vc=lambda a: torch.zeros(4, 65, D, dtype=BF)), "vc must match"),
+    (_mut(inv_freq=lambda a: torch.zeros(129, dtype=F32)), "<= 256"),
+    (_mut(q_out=lambda a: torch.zeros(2, 25 * D, dtype=BF)), "row widths"),
+])
+def test_prep_contract_rejects(native, mutate, msg):
+    with pytest.raises(RuntimeError, match=msg):
+        check_prep(native, mutate(prep_args()))
+
+
+def test_prep_contract_row_limit(native):
+    with pytest.raises(RuntimeError, match="1..8 rows"):
+        check_prep(native, prep_args(n=9))
