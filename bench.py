@@ -1,0 +1,254 @@
+"""Benchmark of the gated-attention decode path on one MI355X.
+
+Workload: split-KV flash-decoding, 1 query row, 24 Q / 4 KV heads, head_dim 256, bf16 KV
+~ N(0,1) at KV lengths 4096 / 16384 / 32768. One "step" is one decode step's attention layers:
+16 layer-calls (attn_decode = partials + gated combine), each on its own KV cache, captured in
+one hipGraph and replayed. The KV buffers rotate over >= 512 MB so the 256 MB Infinity Cache
+cannot serve repeated reads. Inputs are resident in HBM before timing starts.
+
+Printed (one JSON line): value = microseconds per layer-call at KV 16384 (the shortest length
+the >= 75 %-of-HBM target applies to), the sweep at every length, the roofline of the dominant
+kernel (the split-KV partials kernel, timed with HIP events on its stream over a graph of its
+own launches), and the CPU baseline (the reference's PyTorch attention path restated in
+oracle/, on this host's cores, bounded sample).
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--lengths 4096,16384,32768]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HQ, HKV, D = 24, 4, 256
+LAYERS = 16
+ROTATE_BYTES = 512 * 2 ** 20
+HBM_PEAK_GBS = 8000.0
+HEADLINE_L = 16384
+METRIC = "decode-attn µs/layer + achieved HBM GB/s (% of 8 TB/s) at KV 1k–128k"
+
+
+def alg_bytes_layer(L: int, n: int = 1) -> int:
+    """Algorithmic bytes of one decode layer-call: K+V once (4096 B per position for 4 KV heads
+    x 256 dims x 2 tensors x 2 B) plus q, gate and out (12,288 B each per row)."""
+    return 4096 * L + 36864 * n
+
+
+def alg_bytes_partials(L: int, n: int = 1) -> int:
+    """Algorithmic bytes of the split-KV partials kernel: K+V once plus the q rows."""
+    return 4096 * L + 12288 * n
+
+
+def build_if_missing():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("qe_build", ROOT / "qengine_amd" / "_build.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    if not mod.built():
+        mod.build()
+
+
+class LayerSet:
+    """LAYERS layer-calls on distinct KV caches of length L (one graph)."""
+
+    def __init__(self, torch, C, L: int, ns: int, gen):
+        dev = "cuda"
+        BF = torch.bfloat16
+        self.kc = [torch.randn(HKV, L, D, device=dev, generator=gen).to(BF) for _ in range(LAYERS)]
+        self.vc = [torch.randn(HKV, L, D, device=dev, generator=gen).to(BF) for _ in range(LAYERS)]
+        self.q = torch.randn(1, HQ * D, device=dev, generator=gen).to(BF)
+        self.qg = torch.randn(1, HQ * 2 * D, device=dev, generator=gen).to(BF)
+        self.out = torch.empty(1, HQ * D, dtype=BF, device=dev)
+        self.po = torch.empty(1, HQ, ns, D, device=dev)
+        self.pml = torch.empty(1, HQ, ns, 2, device=dev)
+        self.pos = torch.tensor([L - 1], dtype=torch.int32, device=dev)
+        self.C = C
+
+    def decode_all(self):
+        for k, v in zip(self.kc, self.vc):
+            self.C.attn_decode(self.q, k, v, self.pos, self.qg, self.po, self.pml, self.out)
+
+    def partials_all(self):
+        for k, v in zip(self.kc, self.vc):
+            self.C.attn_decode_partials(self.q, k, v, self.pos, self.qg, self.po, self.pml,
+                                        self.out)
+
+
+def capture(torch, fn):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm-up outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def time_graphs(torch, graphs, steps: int, warmup: int) -> float:
+    """Replays graphs round-robin; returns ms per replay over exactly `steps` timed replays.
+    Events are recorded on the current stream, the one the graphs' kernels run on."""
+    for i in range(warmup):
+        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        graphs[i % len(graphs)].replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def bench_length(torch, C, qa, L: int, steps: int, warmup: int, ns: int | None):
+    ns = ns or qa.default_splits(L)
+    nsets = max(1, math.ceil(ROTATE_BYTES / (LAYERS * L * 4096)))
+    gen = torch.Generator(device="cuda").manual_seed(L)
+    sets = [LayerSet(torch, C, L, ns, gen) for _ in range(nsets)]
+    full = [capture(torch, s.decode_all) for s in sets]
+    part = [capture(torch, s.partials_all) for s in sets]
+    ms_step = time_graphs(torch, full, steps, warmup)
+    ms_part = time_graphs(torch, part, steps, warmup)
+    us_layer = ms_step * 1e3 / LAYERS
+    us_part = ms_part * 1e3 / LAYERS
+    res = {
+        "L": L, "NS": ns, "split_size": qa.split_size(L, ns), "kv_rotation_MB":
+            round(nsets * LAYERS * L * 4096 / 2 ** 20, 1),
+        "ms_per_step": ms_step, "us_per_layer": us_layer,
+        "GBps": alg_bytes_layer(L) / (us_layer * 1e3),
+        "partials_us": us_part, "partials_GBps": alg_bytes_partials(L) / (us_part * 1e3),
+    }
+    res["frac"] = res["GBps"] / HBM_PEAK_GBS
+    res["partials_frac"] = res["partials_GBps"] / HBM_PEAK_GBS
+    del sets, full, part
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(torch, L: int, reps: int = 5, warm: int = 2):
+    """The reference's PyTorch attention path (reference.py:263-272, restated op for op in
+    oracle/) timed on this host's CPU cores: one layer-call at KV length L."""
+    import oracle as O
+    torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(L)
+    kc = torch.randn(HKV, L, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(HKV, L, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(HQ, D, generator=g).to(torch.bfloat16)
+    gate = torch.randn(HQ * D, generator=g).to(torch.bfloat16)
+    ts = []
+    for i in range(warm + reps):
+        t0 = time.perf_counter()
+        O.attention_core(q, gate, kc, vc, L)
+        if i >= warm:
+            ts.append(time.perf_counter() - t0)
+    return statistics.median(ts) * 1e6
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def traffic_from_profiles(L: int):
+    """HBM bytes per partials launch measured with rocprofv3 counters (profiles/traffic.json,
+    written from FETCH_SIZE + WRITE_SIZE runs scaled by a copy-kernel calibration), if present."""
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get("partials_bytes_per_launch", {}).get(str(L))
+    except (ValueError, OSError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--lengths", default="4096,16384,32768")
+    ap.add_argument("--ns", type=int, default=0, help="split count (0 = default policy)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build's decode path runs on a single MI355X and "
+              "has no multi-GPU mode (run with --gpus 1).", file=sys.stderr)
+        sys.exit(2)
+
+    build_if_missing()
+    import torch
+    import qengine_amd as qa
+    C = qa._C
+    torch.backends.cuda.matmul.allow_tf32 = False
+    lengths = [int(x) for x in args.lengths.split(",") if x]
+    if HEADLINE_L not in lengths:
+        lengths.append(HEADLINE_L)
+    sweep = []
+    for L in lengths:
+        r = bench_length(torch, C, qa, L, args.steps, args.warmup, args.ns or None)
+        print(f"# L={L}: {r['us_per_layer']:.2f} us/layer-call, {r['GBps']:.0f} GB/s "
+              f"({100 * r['frac']:.1f}%), partials {r['partials_us']:.2f} us "
+              f"({100 * r['partials_frac']:.1f}%)", file=sys.stderr, flush=True)
+        sweep.append(r)
+    head = next(r for r in sweep if r["L"] == HEADLINE_L)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu_us = cpu_baseline(torch, HEADLINE_L)
+        cpu = {"value": cpu_us, "unit": "us/layer-call", "cores": torch.get_num_threads(),
+               "kind": "port",
+               "sample": f"oracle.attention_core (reference.py:263-272 restated in torch, CPU) "
+                         f"at KV {HEADLINE_L}, 1 layer-call, median of 5 after 2 warm-ups",
+               "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count()}
+
+    line = {
+        "metric": METRIC,
+        "value": round(head["us_per_layer"], 3),
+        "unit": "us/layer-call",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "split-KV decode sweep (BASELINE configs[1]), 16 layer-calls "
+                               "per step in one hipGraph", "L": HEADLINE_L, "layers_per_step": LAYERS,
+                   "hq": HQ, "hkv": HKV, "head_dim": D, "rows": 1, "NS": head["NS"],
+                   "split_size": head["split_size"], "kv_rotation_MB": head["kv_rotation_MB"]},
+        "achieved_GBps": round(head["GBps"], 1),
+        "hbm_frac": round(head["frac"], 4),
+        "roofline": {"bound": "hbm", "kernel": "attn_partials_kernel",
+                     "achieved": round(head["partials_GBps"], 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(head["partials_frac"], 4),
+                     "traffic": traffic_from_profiles(HEADLINE_L),
+                     "alg_bytes_per_launch": alg_bytes_partials(HEADLINE_L),
+                     "avg_launch_us": round(head["partials_us"], 3)},
+        "cpu_baseline": cpu,
+        "sweep": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+                  for r in sweep],
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

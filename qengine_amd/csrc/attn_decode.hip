@@ -11,14 +11,16 @@
 //  * The Hq/Hkv query heads of the GQA group times the n rows form the columns of the MFMA tiles
 //    (NT tiles of 16 columns). K and V are read from HBM exactly once per call; Q stays in
 //    registers as an MFMA operand.
-//  * S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x32_bf16. K rows are loaded with 16-byte
-//    buffer loads straight into the MFMA A layout. V is loaded as 16-byte row pieces of 8
-//    positions and regrouped by v_perm into position pairs. With ~6 FLOP per byte, GQA-6 decode
-//    would otherwise need ~70% of the non-packed fp32 VALU peak at 8 TB/s.
+//  * S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x32_bf16. With ~6 FLOP per byte, GQA-6
+//    decode would otherwise need ~70% of the non-packed fp32 VALU peak at 8 TB/s.
+//  * K is read with fully coalesced 16-byte non-temporal buffer loads (two 512-byte rows per
+//    wave instruction) and staged through a per-wave LDS tile with an XOR swizzle, from which
+//    the MFMA operand is read conflict-free. V is loaded straight into registers as 256-byte row
+//    runs of 4 positions and regrouped by v_perm into position pairs for the MFMA A operand.
 //  * Online softmax in the log2 domain per column. Row max/sum reductions over the 4 lane groups
 //    use cross-lane shuffles. Rescaling of the accumulators is skipped when no column's max
 //    moved (an exact no-op).
-//  * Buffer resources bound the K/V reads to the attended range: positions past it load as 0.
+//  * Buffer resources bound the K/V reads to the slice: positions past it load as 0.
 //  * A second launch merges the slices (log-sum-exp) and applies the sigmoid gate.
 #include "qe_device.hpp"
 #include "qe_attn.h"
@@ -28,12 +30,138 @@ namespace qe {
 constexpr int TILE = 32;               // cache positions per wave step (two 16-row MFMA tiles)
 constexpr int WAVES = 4;               // waves per workgroup
 constexpr int THREADS = WAVES * WAVE;  // 256
+constexpr int ROW_CHUNKS = HD * 2 / 16;  // 16-byte chunks per cache row (32)
 
 __host__ __device__ inline int split_size(int max_len, int NS) {
   long per = ((long)max_len + NS - 1) / NS;
   per = (per + TILE - 1) / TILE * TILE;
   return per < TILE ? TILE : (int)per;
 }
+
+// Registers of one wave step (32 cache positions of one KV head).
+struct KVTile {
+  u32x4_t k[16];    // K rows p0 + 2j + lane/32, chunk lane%32 (coalesced; staged through LDS)
+  u32x4_t v[8][2];  // V rows P(g4, e) = p0 + 16(e>>2) + 4g4 + (e&3), dims 128h + 8c + [0, 8)
+};
+
+__device__ __forceinline__ void load_tile(KVTile& b, __amdgpu_buffer_rsrc_t krs,
+                                          __amdgpu_buffer_rsrc_t vrs, int p0, int lane, int c,
+                                          int g4) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j)
+    b.k[j] = buffer_load16_stream(krs, (uint32_t)(p0 + 2 * j) * (HD * 2) + lane * 16);
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      b.v[e][h] = buffer_load16_stream(
+          vrs, (uint32_t)(p0 + 16 * (e >> 2) + 4 * g4 + (e & 3)) * (HD * 2) + (128 * h + 8 * c) * 2);
+}
+
+// LDS slot of (row r, chunk q) in a wave's K tile: chunks are XOR-swizzled by r & 15, so the
+// 16 lanes that read one chunk column of 16 different rows hit 16 different bank groups.
+__device__ __forceinline__ int k_slot(int r, int q) { return r * ROW_CHUNKS + (q ^ (r & 15)); }
+
+// Scores, online softmax and P.V for one tile whose K rows are in the wave's LDS tile `ks_lds`.
+// Column state: running max m (log2 units), running sum l (this lane's 8 positions per tile; the
+// 4 lane groups are summed at the end) and the O^T accumulators acc[ct][h][i] (rows = dims
+// 128h + 32g4 + 8ii + i of column c).
+template <int NT>
+__device__ __forceinline__ void compute_tile(const KVTile& b, const u32x4_t* ks_lds, int p0,
+                                             const int (&Lcol)[NT], const bf16x8_t (&qb)[NT][8],
+                                             float scale_log2, int c, int g4, float (&m)[NT],
+                                             float (&l)[NT], f32x4_t (&acc)[NT][2][8]) {
+  // S^T = K Q^T: A operand row c of M-tile T is position p0 + 16T + c, k-step ks holds dims
+  // [32ks + 8g4, +8). Lane holds positions p0 + 16T + 4g4 + i of column c.
+  f32x4_t sacc[NT][2];
+#pragma unroll
+  for (int T = 0; T < 2; ++T) {
+#pragma unroll
+    for (int ct = 0; ct < NT; ++ct) sacc[ct][T] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const bf16x8_t kop = as_bf16x8(ks_lds[k_slot(16 * T + c, 4 * ks + g4)]);
+#pragma unroll
+      for (int ct = 0; ct < NT; ++ct) sacc[ct][T] = mfma16x16x32(kop, qb[ct][ks], sacc[ct][T]);
+    }
+  }
+
+  // Online softmax per column (log2 domain). P^T goes to the B operand with element e <-> P(g4, e),
+  // as two bf16 terms hi + lo (hi = bf16(p), lo = bf16(p - hi)): ~2^-17 relative error, so P.V
+  // keeps fp32-class accuracy at the cost of a second MFMA per tile.
+  float corr[NT];
+  u32x4_t pb_hi[NT], pb_lo[NT];
+  bool moved = false;
+#pragma unroll
+  for (int ct = 0; ct < NT; ++ct) {
+    float sv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int p = p0 + 16 * (e >> 2) + 4 * g4 + (e & 3);
+      const float x = sacc[ct][e >> 2][e & 3] * scale_log2;
+      sv[e] = p < Lcol[ct] ? x : -INFINITY;
+    }
+    float tmax = sv[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) tmax = fmaxf(tmax, sv[e]);
+    tmax = group4_max(tmax);
+    const float mnew = fmaxf(m[ct], tmax);
+    const float msub = mnew == -INFINITY ? 0.f : mnew;
+    corr[ct] = mnew == m[ct] ? 1.f : __builtin_amdgcn_exp2f(m[ct] - msub);
+    moved |= corr[ct] != 1.f;
+    float pf[8], plo[8];
+    float lsum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      pf[e] = __builtin_amdgcn_exp2f(sv[e] - msub);
+      lsum += pf[e];
+      plo[e] = pf[e] - round_bf16(pf[e]);
+    }
+    l[ct] = l[ct] * corr[ct] + lsum;
+    m[ct] = mnew;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      pb_hi[ct][d] = pack_bf16x2(pf[2 * d], pf[2 * d + 1]);
+      pb_lo[ct][d] = pack_bf16x2(plo[2 * d], plo[2 * d + 1]);
+    }
+  }
+  if (__any(moved)) {  // exact no-op when no column's max moved, so skipped
+#pragma unroll
+    for (int ct = 0; ct < NT; ++ct)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[ct][h][i] *= corr[ct];
+  }
+
+  // O^T += V^T P^T. A-operand row c of tile (h, i) is dim 128h + 8c + i over the 8 positions.
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      u32x4_t a;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        a[d] = interleave_halves(b.v[2 * d][h][i >> 1], b.v[2 * d + 1][h][i >> 1], i & 1);
+#pragma unroll
+      for (int ct = 0; ct < NT; ++ct) {
+        acc[ct][h][i] = mfma16x16x32(as_bf16x8(a), as_bf16x8(pb_hi[ct]), acc[ct][h][i]);
+        acc[ct][h][i] = mfma16x16x32(as_bf16x8(a), as_bf16x8(pb_lo[ct]), acc[ct][h][i]);
+      }
+    }
+}
+
+// Order this wave's LDS accesses: the compiler must not move LDS reads/writes across it (lanes
+// exchange data through LDS, which single-thread alias analysis cannot see).
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// LDS: per-wave K tiles during the loop; reused for the cross-wave merge afterwards.
+constexpr int LDS_K_BYTES = WAVES * TILE * HD * 2;     // 64 KB
+constexpr int LDS_MERGE_BYTES = WAVES * 32 * WAVE * 4; // 32 KB
+static_assert(LDS_MERGE_BYTES <= LDS_K_BYTES, "merge buffer aliases the K tiles");
 
 // part_o [n][Hq][NS][HD] (unnormalised O), part_ml [n][Hq][NS][2] = (max in log2 units, sum).
 template <int NT>
@@ -53,6 +181,10 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc
   const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
   const int c = lane & 15, g4 = lane >> 4;
   const int ncols = grp * n;
+
+  __shared__ __attribute__((aligned(16))) char lds[LDS_K_BYTES];
+  __shared__ float s_m[WAVES][16 * NT], s_l[WAVES][16 * NT];
+  u32x4_t* ks_lds = reinterpret_cast<u32x4_t*>(lds) + w * TILE * ROW_CHUNKS;
 
   // Q^T as the MFMA B operand. Column ct*16+c is (row t, head g*grp+j), col = t*grp + j.
   // Lane group g4 holds dims [32ks + 8g4, +8) of k-step ks (the same dims as the K operand).
@@ -76,12 +208,12 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc
   }
 
   const size_t head_off = (size_t)g * max_len * HD;
-  const uint32_t bytes = (uint32_t)Lmax * (uint32_t)(HD * 2);
+  const uint32_t bytes = (uint32_t)end * (uint32_t)(HD * 2);  // loads past the slice read 0
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(kc + head_off, bytes);
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vc + head_off, bytes);
 
   float m[NT], l[NT];
-  f32x4_t acc[NT][2][8];  // O^T: [ct][half h][i] rows = dims 128h + 32g4 + 8ii + i, col c
+  f32x4_t acc[NT][2][8];
 #pragma unroll
   for (int ct = 0; ct < NT; ++ct) {
     m[ct] = -INFINITY;
@@ -93,105 +225,19 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc
   }
 
   for (int p0 = beg + w * TILE; p0 < end; p0 += WAVES * TILE) {
-    // K: A-operand rows p0 + 16T + c, dims [32ks + 8g4, +8).
-    u32x4_t kr[2][8];
+    KVTile buf;
+    load_tile(buf, krs, vrs, p0, lane, c, g4);
+    wave_lds_fence();  // the previous tile's K reads are done before this tile's writes
 #pragma unroll
-    for (int T = 0; T < 2; ++T)
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks)
-        kr[T][ks] = buffer_load16(krs, (uint32_t)(p0 + 16 * T + c) * (HD * 2) + (4 * ks + g4) * 16);
-    // V: 8 positions per lane, P(g4, e) = p0 + 16(e>>2) + 4g4 + (e&3), dims 128h + 8c + [0,8).
-    u32x4_t vr[8][2];
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-        vr[e][h] = buffer_load16(
-            vrs, (uint32_t)(p0 + 16 * (e >> 2) + 4 * g4 + (e & 3)) * (HD * 2) + (128 * h + 8 * c) * 2);
-
-    // S^T = K Q^T: lane holds positions p0 + 16T + 4g4 + i of column c.
-    f32x4_t sacc[NT][2];
-#pragma unroll
-    for (int ct = 0; ct < NT; ++ct)
-#pragma unroll
-      for (int T = 0; T < 2; ++T) {
-        f32x4_t a = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) a = mfma16x16x32(as_bf16x8(kr[T][ks]), qb[ct][ks], a);
-        sacc[ct][T] = a;
-      }
-
-    // Online softmax per column (log2 domain). P^T goes to the B operand with element e <-> P(g4, e),
-    // as two bf16 terms hi + lo (hi = bf16(p), lo = bf16(p - hi)): ~2^-17 relative error, so P.V
-    // keeps fp32-class accuracy at the cost of a second MFMA per tile.
-    float corr[NT];
-    u32x4_t pb_hi[NT], pb_lo[NT];
-    bool moved = false;
-#pragma unroll
-    for (int ct = 0; ct < NT; ++ct) {
-      float sv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int p = p0 + 16 * (e >> 2) + 4 * g4 + (e & 3);
-        const float x = sacc[ct][e >> 2][e & 3] * scale_log2;
-        sv[e] = p < Lcol[ct] ? x : -INFINITY;
-      }
-      float tmax = sv[0];
-#pragma unroll
-      for (int e = 1; e < 8; ++e) tmax = fmaxf(tmax, sv[e]);
-      tmax = group4_max(tmax);
-      const float mnew = fmaxf(m[ct], tmax);
-      const float msub = mnew == -INFINITY ? 0.f : mnew;
-      corr[ct] = mnew == m[ct] ? 1.f : __builtin_amdgcn_exp2f(m[ct] - msub);
-      moved |= corr[ct] != 1.f;
-      float pf[8], plo[8];
-      float lsum = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        pf[e] = __builtin_amdgcn_exp2f(sv[e] - msub);
-        lsum += pf[e];
-        plo[e] = pf[e] - round_bf16(pf[e]);
-      }
-      l[ct] = l[ct] * corr[ct] + lsum;
-      m[ct] = mnew;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        pb_hi[ct][d] = pack_bf16x2(pf[2 * d], pf[2 * d + 1]);
-        pb_lo[ct][d] = pack_bf16x2(plo[2 * d], plo[2 * d + 1]);
-      }
-    }
-    if (__any(moved)) {
-#pragma unroll
-      for (int ct = 0; ct < NT; ++ct)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int i = 0; i < 8; ++i) acc[ct][h][i] *= corr[ct];
-    }
-
-    // O^T += V^T P^T. A-operand row c of tile (h, i) is dim 128h + 8c + i over the 8 positions.
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        u32x4_t a;
-#pragma unroll
-        for (int d = 0; d < 4; ++d)
-          a[d] = interleave_halves(vr[2 * d][h][i >> 1], vr[2 * d + 1][h][i >> 1], i & 1);
-#pragma unroll
-        for (int ct = 0; ct < NT; ++ct) {
-          acc[ct][h][i] = mfma16x16x32(as_bf16x8(a), as_bf16x8(pb_hi[ct]), acc[ct][h][i]);
-          acc[ct][h][i] = mfma16x16x32(as_bf16x8(a), as_bf16x8(pb_lo[ct]), acc[ct][h][i]);
-        }
-      }
+    for (int j = 0; j < 16; ++j) ks_lds[k_slot(2 * j + (lane >> 5), lane & 31)] = buf.k[j];
+    wave_lds_fence();
+    compute_tile<NT>(buf, ks_lds, p0, Lcol, qb, scale_log2, c, g4, m, l, acc);
   }
 
   // ---- merge the waves of this workgroup in a fixed order and write the slice's partial
 #pragma unroll
   for (int ct = 0; ct < NT; ++ct) l[ct] = group4_sum(l[ct]);
 
-  __shared__ float s_m[WAVES][16 * NT], s_l[WAVES][16 * NT];
-  __shared__ float s_acc[WAVES][32][WAVE];
   if (g4 == 0) {
 #pragma unroll
     for (int ct = 0; ct < NT; ++ct) {
@@ -199,7 +245,7 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc
       s_l[w][ct * 16 + c] = l[ct];
     }
   }
-  __syncthreads();
+  __syncthreads();  // also: every wave is done with its K tile, so `lds` can hold the merge
 
   float wsc[NT][WAVES];
 #pragma unroll
@@ -223,6 +269,7 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc
     }
   }
 
+  float (*s_acc)[32][WAVE] = reinterpret_cast<float (*)[32][WAVE]>(lds);
 #pragma unroll
   for (int ct = 0; ct < NT; ++ct) {
     const int col = ct * 16 + c;
@@ -254,29 +301,79 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc
 }
 
 // Log-sum-exp merge of the slices holding row t's positions + fused sigmoid output gate.
-__global__ void __launch_bounds__(HD)
+// One wave per (head h, row t, 64-dim chunk z). Lane group sg = lane/16 owns slices
+// s = sg (mod 4) and 4 dims per lane. The loads of a batch of COMBINE_BATCH slices are all
+// issued before any of them is used, so up to 4*COMBINE_BATCH slices cost one memory round trip.
+// The groups are added in a fixed order, so the result depends only on row t's partials and slice
+// count, never on the other rows of the call.
+constexpr int COMBINE_DIMS = 64;
+constexpr int COMBINE_BATCH = 16;
+
+__global__ void __launch_bounds__(WAVE)
 attn_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml,
                     const int* __restrict__ pos_ptr, const __bf16* __restrict__ qg, long ldp,
                     __bf16* __restrict__ out, long ldo, int Hq, int max_len, int NS, int CH) {
-  const int h = blockIdx.x, t = blockIdx.y, c = threadIdx.x;
+  const int h = blockIdx.x, t = blockIdx.y, z = blockIdx.z;
+  const int lane = threadIdx.x, c16 = lane & 15, sg = lane >> 4;
   const int L_t = min(pos_ptr[0] + t + 1, max_len);
   const int S = L_t > 0 ? (L_t + CH - 1) / CH : 0;
   const size_t base = ((size_t)t * Hq + h) * NS;
   const float* ml = part_ml + base * 2;
-  float M = -INFINITY;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, ml[2 * s]);
-  float L = 0.f, O = 0.f;
-  for (int s = 0; s < S; ++s) {
-    const float ms = ml[2 * s];
-    if (ms == -INFINITY) continue;
-    const float f = __builtin_amdgcn_exp2f(ms - M);
-    L += ml[2 * s + 1] * f;
-    O += part_o[(base + s) * HD + c] * f;
+  const int dim = z * COMBINE_DIMS + 4 * c16;
+  const __bf16* gp = qg + (size_t)t * ldp + (size_t)h * 2 * HD + HD + dim;
+  float gate[4];  // loaded early; qg rows carry no alignment guarantee beyond 2 bytes
+#pragma unroll
+  for (int i = 0; i < 4; ++i) gate[i] = bf16_to_f32(gp[i]);
+
+  f32x4_t O = {0.f, 0.f, 0.f, 0.f};
+  float L = 0.f, M = -INFINITY;
+  for (int s0 = 0; s0 < S; s0 += 4 * COMBINE_BATCH) {
+    f32x4_t po[COMBINE_BATCH];
+    float2 mls[COMBINE_BATCH];
+#pragma unroll
+    for (int b = 0; b < COMBINE_BATCH; ++b) {
+      const int s = s0 + 4 * b + sg;
+      if (s < S) {
+        po[b] = *reinterpret_cast<const f32x4_t*>(part_o + (base + s) * HD + dim);
+        mls[b] = *reinterpret_cast<const float2*>(ml + 2 * s);
+      } else {
+        po[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        mls[b] = make_float2(-INFINITY, 0.f);
+      }
+    }
+    // running max over all slices seen so far (every lane group, so M is wave-uniform)
+    float bm = M;
+#pragma unroll
+    for (int b = 0; b < COMBINE_BATCH; ++b) bm = fmaxf(bm, mls[b].x);
+    bm = fmaxf(bm, __shfl_xor(bm, 16));
+    bm = fmaxf(bm, __shfl_xor(bm, 32));
+    if (bm != M) {  // rescale what was accumulated under the old max (exact no-op otherwise)
+      const float r = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - bm);
+      O *= r;
+      L *= r;
+      M = bm;
+    }
+#pragma unroll
+    for (int b = 0; b < COMBINE_BATCH; ++b) {
+      const float f = mls[b].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mls[b].x - M);
+      L += mls[b].y * f;
+      O += po[b] * f;
+    }
   }
-  const float o = round_bf16(O / L);
-  const float gate = bf16_to_f32(qg[(size_t)t * ldp + (size_t)h * 2 * HD + HD + c]);
-  const float sg = round_bf16(sigmoid_f32(gate));
-  out[(size_t)t * ldo + (size_t)h * HD + c] = f32_to_bf16(o * sg);
+#pragma unroll
+  for (int o = 16; o <= 32; o <<= 1) {
+    L += __shfl_xor(L, o);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) O[i] += __shfl_xor(O[i], o);
+  }
+  if (sg == 0) {
+    __bf16* op = out + (size_t)t * ldo + (size_t)h * HD + dim;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float o = round_bf16(O[i] / L);  // attention output is a bf16 tensor
+      op[i] = f32_to_bf16(o * round_bf16(sigmoid_f32(gate[i])));
+    }
+  }
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -285,8 +382,9 @@ static hipError_t check_decode_shape(int n, int Hq, int Hkv, int max_len, int NS
   if (n < 1 || n > 8 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || NS < 1 || max_len < 1)
     return hipErrorInvalidValue;
   if ((Hq / Hkv) * n > 64) return hipErrorInvalidValue;            // at most 4 column tiles
-  // byte offsets (including the tile overhang past max_len) must fit the 32-bit buffer range
-  if ((unsigned long long)(max_len + TILE) * HD * 2 >= (1ull << 32)) return hipErrorInvalidValue;
+  // byte offsets of the last tile (up to one tile past max_len) must fit the 32-bit buffer range
+  if ((unsigned long long)(max_len + TILE) * HD * 2 >= (1ull << 32))
+    return hipErrorInvalidValue;
   return hipSuccess;
 }
 
@@ -314,7 +412,7 @@ static hipError_t launch_combine(const float* part_o, const float* part_ml, cons
                                  const void* qg, long ldp, void* out, long ldo, int n, int Hq,
                                  int max_len, int NS, hipStream_t stream) {
   const int CH = split_size(max_len, NS);
-  attn_combine_kernel<<<dim3(Hq, n), dim3(HD), 0, stream>>>(
+  attn_combine_kernel<<<dim3(Hq, n, HD / COMBINE_DIMS), dim3(WAVE), 0, stream>>>(
       part_o, part_ml, pos, static_cast<const __bf16*>(qg), ldp, static_cast<__bf16*>(out), ldo,
       Hq, max_len, NS, CH);
   return hipGetLastError();
