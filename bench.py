@@ -113,7 +113,7 @@ def time_graphs(torch, graphs, steps: int, warmup: int) -> float:
 
 
 def bench_length(torch, C, qa, L: int, steps: int, warmup: int, ns: int | None):
-    ns = ns or qa.default_splits(L)
+    ns = ns or qa.default_splits(L, HKV)
     nsets = max(1, math.ceil(ROTATE_BYTES / (LAYERS * L * 4096)))
     gen = torch.Generator(device="cuda").manual_seed(L)
     sets = [LayerSet(torch, C, L, ns, gen) for _ in range(nsets)]

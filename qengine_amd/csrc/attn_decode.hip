@@ -14,8 +14,9 @@
 //  * S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x32_bf16. With ~6 FLOP per byte, GQA-6
 //    decode would otherwise need ~70% of the non-packed fp32 VALU peak at 8 TB/s.
 //  * K is read with fully coalesced 16-byte non-temporal buffer loads (two 512-byte rows per
-//    wave instruction) and staged through a per-wave LDS tile with an XOR swizzle, from which
-//    the MFMA operand is read conflict-free. V is loaded straight into registers as 256-byte row
+//    wave instruction) that write straight into a per-wave LDS tile (LDS DMA, no registers);
+//    the lane-to-address assignment applies an XOR swizzle, so the MFMA operand is read from LDS
+//    without bank conflicts. V is loaded straight into registers as 256-byte row
 //    runs of 4 positions and regrouped by v_perm into position pairs for the MFMA A operand.
 //  * Online softmax in the log2 domain per column. Row max/sum reductions over the 4 lane groups
 //    use cross-lane shuffles. Rescaling of the accumulators is skipped when no column's max
@@ -28,8 +29,12 @@
 namespace qe {
 
 constexpr int TILE = 32;               // cache positions per wave step (two 16-row MFMA tiles)
-constexpr int WAVES = 4;               // waves per workgroup
-constexpr int THREADS = WAVES * WAVE;  // 256
+// Waves per workgroup. Tile k of a slice goes to wave k % 4 and the waves are merged in order
+// 0..3 for every column-tile count NT: the within-slice decomposition (and so every rounding)
+// is the same for 1 row and for 8, which is what keeps row t of an n-row call bit-identical to
+// a 1-row call. (Eight waves for NT = 1 were measured no faster on MI355X.)
+template <int NT>
+constexpr int waves_for() { return 4; }
 constexpr int ROW_CHUNKS = HD * 2 / 16;  // 16-byte chunks per cache row (32)
 
 __host__ __device__ inline int split_size(int max_len, int NS) {
@@ -38,18 +43,27 @@ __host__ __device__ inline int split_size(int max_len, int NS) {
   return per < TILE ? TILE : (int)per;
 }
 
-// Registers of one wave step (32 cache positions of one KV head).
-struct KVTile {
-  u32x4_t k[16];    // K rows p0 + 2j + lane/32, chunk lane%32 (coalesced; staged through LDS)
+// Registers of one wave step (32 cache positions of one KV head). K goes straight to LDS.
+struct VTile {
   u32x4_t v[8][2];  // V rows P(g4, e) = p0 + 16(e>>2) + 4g4 + (e&3), dims 128h + 8c + [0, 8)
 };
 
-__device__ __forceinline__ void load_tile(KVTile& b, __amdgpu_buffer_rsrc_t krs,
+// LDS slot of (row r, chunk q) in a wave's K tile: chunks are XOR-swizzled by r & 15, so the
+// 16 lanes that read one chunk column of 16 different rows hit 16 different bank groups.
+__device__ __forceinline__ int k_slot(int r, int q) { return r * ROW_CHUNKS + (q ^ (r & 15)); }
+
+// Issue one tile's loads: 16 LDS-DMA loads of K (instruction j covers rows 2j, 2j+1: lane i
+// fetches the chunk that belongs in LDS slot 64j + i, so each instruction reads 1 KB of
+// contiguous cache), then 16 register loads of V (4 rows x 256 B per instruction).
+__device__ __forceinline__ void load_tile(VTile& b, u32x4_t* ks_lds, __amdgpu_buffer_rsrc_t krs,
                                           __amdgpu_buffer_rsrc_t vrs, int p0, int lane, int c,
                                           int g4) {
 #pragma unroll
-  for (int j = 0; j < 16; ++j)
-    b.k[j] = buffer_load16_stream(krs, (uint32_t)(p0 + 2 * j) * (HD * 2) + lane * 16);
+  for (int j = 0; j < 16; ++j) {
+    const int r = 2 * j + (lane >> 5);
+    const int q = (lane & 31) ^ (r & 15);
+    buffer_load16_to_lds(krs, (uint32_t)(p0 + r) * (HD * 2) + q * 16, ks_lds + 64 * j);
+  }
 #pragma unroll
   for (int e = 0; e < 8; ++e)
 #pragma unroll
@@ -58,16 +72,12 @@ __device__ __forceinline__ void load_tile(KVTile& b, __amdgpu_buffer_rsrc_t krs,
           vrs, (uint32_t)(p0 + 16 * (e >> 2) + 4 * g4 + (e & 3)) * (HD * 2) + (128 * h + 8 * c) * 2);
 }
 
-// LDS slot of (row r, chunk q) in a wave's K tile: chunks are XOR-swizzled by r & 15, so the
-// 16 lanes that read one chunk column of 16 different rows hit 16 different bank groups.
-__device__ __forceinline__ int k_slot(int r, int q) { return r * ROW_CHUNKS + (q ^ (r & 15)); }
-
 // Scores, online softmax and P.V for one tile whose K rows are in the wave's LDS tile `ks_lds`.
 // Column state: running max m (log2 units), running sum l (this lane's 8 positions per tile; the
 // 4 lane groups are summed at the end) and the O^T accumulators acc[ct][h][i] (rows = dims
 // 128h + 32g4 + 8ii + i of column c).
 template <int NT>
-__device__ __forceinline__ void compute_tile(const KVTile& b, const u32x4_t* ks_lds, int p0,
+__device__ __forceinline__ void compute_tile(const VTile& b, const u32x4_t* ks_lds, int p0,
                                              const int (&Lcol)[NT], const bf16x8_t (&qb)[NT][8],
                                              float scale_log2, int c, int g4, float (&m)[NT],
                                              float (&l)[NT], f32x4_t (&acc)[NT][2][8]) {
@@ -158,14 +168,30 @@ __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_wave_barrier();
 }
 
+// Wait for the tile's K (its 16 LDS-DMA loads were issued before the 16 V loads, so at most 16
+// loads may remain in flight), then compute the tile.
+template <int NT>
+__device__ __forceinline__ void wait_and_compute(const VTile& b, const u32x4_t* ks_lds, int p0,
+                                                 const int (&Lcol)[NT],
+                                                 const bf16x8_t (&qb)[NT][8], float scale_log2,
+                                                 int c, int g4, float (&m)[NT], float (&l)[NT],
+                                                 f32x4_t (&acc)[NT][2][8]) {
+  vmcnt_wait<16>();
+  wave_lds_fence();
+  compute_tile<NT>(b, ks_lds, p0, Lcol, qb, scale_log2, c, g4, m, l, acc);
+  wave_lds_fence();  // this tile's K reads happen before the next tile's LDS-DMA writes
+}
+
 // LDS: per-wave K tiles during the loop; reused for the cross-wave merge afterwards.
-constexpr int LDS_K_BYTES = WAVES * TILE * HD * 2;     // 64 KB
-constexpr int LDS_MERGE_BYTES = WAVES * 32 * WAVE * 4; // 32 KB
-static_assert(LDS_MERGE_BYTES <= LDS_K_BYTES, "merge buffer aliases the K tiles");
+template <int WAVES>
+constexpr int lds_k_bytes() { return WAVES * TILE * HD * 2; }  // 16 KB per wave
+static_assert(4 * 32 * WAVE * 4 <= lds_k_bytes<4>(), "merge buffer aliases the K tiles");
 
 // part_o [n][Hq][NS][HD] (unnormalised O), part_ml [n][Hq][NS][2] = (max in log2 units, sum).
-template <int NT>
-__global__ void __launch_bounds__(THREADS)
+// NT = 1 (decode, 1-2 rows) fits in 256 registers, which lets two workgroups share a CU (one
+// streams while the other computes); the multi-row verify shapes need the whole register file.
+template <int NT, int WAVES = waves_for<NT>()>
+__global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, 2)))
 attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
                      const __bf16* __restrict__ vc, const int* __restrict__ pos_ptr,
                      float* __restrict__ part_o, float* __restrict__ part_ml, int n, int Hq,
@@ -182,7 +208,7 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc
   const int c = lane & 15, g4 = lane >> 4;
   const int ncols = grp * n;
 
-  __shared__ __attribute__((aligned(16))) char lds[LDS_K_BYTES];
+  __shared__ __attribute__((aligned(16))) char lds[lds_k_bytes<WAVES>()];
   __shared__ float s_m[WAVES][16 * NT], s_l[WAVES][16 * NT];
   u32x4_t* ks_lds = reinterpret_cast<u32x4_t*>(lds) + w * TILE * ROW_CHUNKS;
 
@@ -225,13 +251,9 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc
   }
 
   for (int p0 = beg + w * TILE; p0 < end; p0 += WAVES * TILE) {
-    KVTile buf;
-    load_tile(buf, krs, vrs, p0, lane, c, g4);
-    wave_lds_fence();  // the previous tile's K reads are done before this tile's writes
-#pragma unroll
-    for (int j = 0; j < 16; ++j) ks_lds[k_slot(2 * j + (lane >> 5), lane & 31)] = buf.k[j];
-    wave_lds_fence();
-    compute_tile<NT>(buf, ks_lds, p0, Lcol, qb, scale_log2, c, g4, m, l, acc);
+    VTile buf;
+    load_tile(buf, ks_lds, krs, vrs, p0, lane, c, g4);
+    wait_and_compute<NT>(buf, ks_lds, p0, Lcol, qb, scale_log2, c, g4, m, l, acc);
   }
 
   // ---- merge the waves of this workgroup in a fixed order and write the slice's partial
@@ -280,20 +302,24 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) s_acc[w][i * 4 + ii][lane] = acc[ct][h][i][ii];
       __syncthreads();
-      // this thread merges ii = w for i = 0..7: dims 128h + 32g4 + 8w + [0, 8)
-      float o[8];
+      // this thread merges ii = w % 4 for VPT consecutive i: dims 128h + 32g4 + 8ii + i
+      constexpr int VPT = 32 / WAVES;
+      const int ii = w & 3, i0 = (w >> 2) * VPT;
+      float o[VPT];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int k = 0; k < VPT; ++k) {
         float sum = 0.f;
 #pragma unroll
-        for (int v = 0; v < WAVES; ++v) sum += s_acc[v][i * 4 + w][lane] * wsc[ct][v];
-        o[i] = sum;
+        for (int v = 0; v < WAVES; ++v) sum += s_acc[v][(i0 + k) * 4 + ii][lane] * wsc[ct][v];
+        o[k] = sum;
       }
       if (col < ncols) {
         const int t = col / grp, head = g * grp + (col - t * grp);
-        float* dst = part_o + (((size_t)t * Hq + head) * NS + s) * HD + 128 * h + 32 * g4 + 8 * w;
-        reinterpret_cast<f32x4_t*>(dst)[0] = f32x4_t{o[0], o[1], o[2], o[3]};
-        reinterpret_cast<f32x4_t*>(dst)[1] = f32x4_t{o[4], o[5], o[6], o[7]};
+        float* dst =
+            part_o + (((size_t)t * Hq + head) * NS + s) * HD + 128 * h + 32 * g4 + 8 * ii + i0;
+#pragma unroll
+        for (int k = 0; k < VPT; k += 4)
+          reinterpret_cast<f32x4_t*>(dst)[k / 4] = f32x4_t{o[k], o[k + 1], o[k + 2], o[k + 3]};
       }
       __syncthreads();
     }
@@ -315,36 +341,44 @@ attn_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ 
                     __bf16* __restrict__ out, long ldo, int Hq, int max_len, int NS, int CH) {
   const int h = blockIdx.x, t = blockIdx.y, z = blockIdx.z;
   const int lane = threadIdx.x, c16 = lane & 15, sg = lane >> 4;
-  const int L_t = min(pos_ptr[0] + t + 1, max_len);
-  const int S = L_t > 0 ? (L_t + CH - 1) / CH : 0;
   const size_t base = ((size_t)t * Hq + h) * NS;
   const float* ml = part_ml + base * 2;
   const int dim = z * COMBINE_DIMS + 4 * c16;
   const __bf16* gp = qg + (size_t)t * ldp + (size_t)h * 2 * HD + HD + dim;
-  float gate[4];  // loaded early; qg rows carry no alignment guarantee beyond 2 bytes
+
+  // The first batch of slices is loaded before pos arrives (every slot below NS exists in the
+  // caller's buffers); slots past row t's slice count S are discarded by selection, so stale
+  // contents never reach the sums.
+  f32x4_t po[COMBINE_BATCH];
+  float2 mls[COMBINE_BATCH];
+  auto load_batch = [&](int s0, int lim) {
+#pragma unroll
+    for (int b = 0; b < COMBINE_BATCH; ++b) {
+      const int s = s0 + 4 * b + sg;
+      if (s < lim) {
+        po[b] = *reinterpret_cast<const f32x4_t*>(part_o + (base + s) * HD + dim);
+        mls[b] = *reinterpret_cast<const float2*>(ml + 2 * s);
+      }
+    }
+  };
+  load_batch(0, NS);
+  float gate[4];  // qg rows carry no alignment guarantee beyond 2 bytes
 #pragma unroll
   for (int i = 0; i < 4; ++i) gate[i] = bf16_to_f32(gp[i]);
+  const int L_t = min(pos_ptr[0] + t + 1, max_len);
+  const int S = L_t > 0 ? (L_t + CH - 1) / CH : 0;
 
   f32x4_t O = {0.f, 0.f, 0.f, 0.f};
   float L = 0.f, M = -INFINITY;
   for (int s0 = 0; s0 < S; s0 += 4 * COMBINE_BATCH) {
-    f32x4_t po[COMBINE_BATCH];
-    float2 mls[COMBINE_BATCH];
+    if (s0 > 0) load_batch(s0, S);
+    bool valid[COMBINE_BATCH];
 #pragma unroll
-    for (int b = 0; b < COMBINE_BATCH; ++b) {
-      const int s = s0 + 4 * b + sg;
-      if (s < S) {
-        po[b] = *reinterpret_cast<const f32x4_t*>(part_o + (base + s) * HD + dim);
-        mls[b] = *reinterpret_cast<const float2*>(ml + 2 * s);
-      } else {
-        po[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        mls[b] = make_float2(-INFINITY, 0.f);
-      }
-    }
+    for (int b = 0; b < COMBINE_BATCH; ++b) valid[b] = s0 + 4 * b + sg < S;
     // running max over all slices seen so far (every lane group, so M is wave-uniform)
     float bm = M;
 #pragma unroll
-    for (int b = 0; b < COMBINE_BATCH; ++b) bm = fmaxf(bm, mls[b].x);
+    for (int b = 0; b < COMBINE_BATCH; ++b) bm = valid[b] ? fmaxf(bm, mls[b].x) : bm;
     bm = fmaxf(bm, __shfl_xor(bm, 16));
     bm = fmaxf(bm, __shfl_xor(bm, 32));
     if (bm != M) {  // rescale what was accumulated under the old max (exact no-op otherwise)
@@ -355,9 +389,11 @@ attn_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ 
     }
 #pragma unroll
     for (int b = 0; b < COMBINE_BATCH; ++b) {
-      const float f = mls[b].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mls[b].x - M);
-      L += mls[b].y * f;
-      O += po[b] * f;
+      if (valid[b] && mls[b].x != -INFINITY) {
+        const float f = __builtin_amdgcn_exp2f(mls[b].x - M);
+        L += mls[b].y * f;
+        O += po[b] * f;
+      }
     }
   }
 #pragma unroll
@@ -393,17 +429,17 @@ static hipError_t launch_partials(const void* q, const void* kc, const void* vc,
                                   int max_len, int NS, float scale, hipStream_t stream) {
   const int CH = split_size(max_len, NS);
   const int slices = (max_len + CH - 1) / CH;  // <= NS; later slices never hold positions
-  const dim3 grid(slices, Hkv), block(THREADS);
+  const dim3 grid(slices, Hkv);
   const float scale_log2 = scale * 1.4426950408889634f;
   const int NT = ((Hq / Hkv) * n + 15) / 16;
   const auto* Q = static_cast<const __bf16*>(q);
   const auto* K = static_cast<const __bf16*>(kc);
   const auto* V = static_cast<const __bf16*>(vc);
   switch (NT) {
-    case 1: attn_partials_kernel<1><<<grid, block, 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
-    case 2: attn_partials_kernel<2><<<grid, block, 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
-    case 3: attn_partials_kernel<3><<<grid, block, 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
-    default: attn_partials_kernel<4><<<grid, block, 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
+    case 1: attn_partials_kernel<1><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
+    case 2: attn_partials_kernel<2><<<grid, dim3(waves_for<2>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
+    case 3: attn_partials_kernel<3><<<grid, dim3(waves_for<3>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
+    default: attn_partials_kernel<4><<<grid, dim3(waves_for<4>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
   }
   return hipGetLastError();
 }

@@ -75,6 +75,23 @@ __device__ __forceinline__ u32x4_t buffer_load16_stream(__amdgpu_buffer_rsrc_t r
       u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, CPOL_NT));
 }
 
+// 16 bytes per lane from a buffer straight into LDS (gfx950 LDS DMA, non-temporal): lane i of the
+// wave writes lds_base + 16*i. lds_base must be wave-uniform. The compiler does not order later
+// LDS reads after this write: wait with vmcnt_wait() first.
+__device__ __forceinline__ void buffer_load16_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t byte_off,
+                                                     void* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void*)lds_base, 16, (int)byte_off, 0, 0, CPOL_NT);
+}
+
+// s_waitcnt vmcnt(N): at most N vector-memory loads of this wave still outstanding (gfx9
+// encoding: vmcnt low bits [3:0], high bits [15:14]; expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void vmcnt_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
 
 // D = A(16x32) * B(32x16) + C on bf16 inputs with fp32 accumulation. Lane l holds A row l%16 /
