@@ -186,11 +186,25 @@ def main():
     ap.add_argument("--lengths", default="4096,16384,32768")
     ap.add_argument("--ns", type=int, default=0, help="split count (0 = default policy)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 5 plain device copies of MIB MiB (reads MIB, writes MIB): the "
+                         "reference kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE to bytes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build's decode path runs on a single MI355X and "
               "has no multi-GPU mode (run with --gpus 1).", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_calibration:
+        import torch
+        n = args.copy_calibration * 2 ** 20 // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_MiB": args.copy_calibration, "launches": 5}))
+        return
 
     build_if_missing()
     import torch

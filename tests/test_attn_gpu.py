@@ -333,3 +333,43 @@ def test_graph_capture_replays(native):
         eager[4].add_(1)
         graphed[4].add_(1)
         torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------------ the engine's attention branch
+def test_layer_multi_row_passes_match_token_by_token(native):
+    """The reference's 27B layer test shape (tests/test_27b_layers.py:113-162 of qengine) without
+    weights: passes of [1, 4, 8, 2, 8, 1, 8] rows through GatedAttention (prep + decode, the
+    engine's attention branch) against the oracle run one token at a time (attention_step:
+    write the cache at pos, attend [0, pos]); the caches must agree too."""
+    from qengine_amd.layer import GatedAttention
+    hq, hkv, T = 24, 4, 32
+    g = gen(41)
+    qnw, knw = norm_weights(g)
+    layer = GatedAttention(hq, hkv, max_len=T, q_norm=qnw, k_norm=knw, splits=4)
+    pr_all = proj_rows(g, T, hq, hkv)
+    inv = O.rope_inv_freq(1e7, 64)
+    kc_ref = torch.zeros(hkv, T, D, dtype=BF)
+    vc_ref = torch.zeros_like(kc_ref)
+    refs = []
+    for t in range(T):
+        q_r = O.attn_prep(pr_all.qg[t], pr_all.k[t], pr_all.v[t], qnw, knw, inv, t, kc_ref, vc_ref,
+                          1e-6, hq)
+        refs.append(O.attn_decode(q_r, kc_ref, vc_ref, t, pr_all.qg[t], hq)[0])
+    proj_d = _dev(pr_all.proj)
+    pos = torch.zeros(1, dtype=torch.int32, device=DEV)
+    outs, t = [], 0
+    for n in [1, 4, 8, 2, 8, 1, 8]:
+        n = min(n, T - t)
+        if n == 0:
+            break
+        pos.fill_(t)
+        out = torch.empty(n, hq * D, dtype=BF, device=DEV)
+        layer(proj_d[t:t + n], pos, out)
+        outs.append(out.cpu())
+        t += n
+    got = torch.cat(outs)
+    ok, mx, mean = attn_close(got, torch.stack(refs))
+    assert ok, (mx, mean)
+    ok, err = ulp_close(layer.kc.cpu(), kc_ref, ulps=1)
+    assert ok, err
+    assert torch.equal(layer.vc.cpu(), vc_ref)
