@@ -137,6 +137,110 @@ def bench_length(torch, C, qa, L: int, steps: int, warmup: int, ns: int | None):
     return res
 
 
+def time_fn_graph(torch, fn, steps: int, warmup: int) -> float:
+    """ms per replay of a graph capturing fn()."""
+    return time_graphs(torch, [capture(torch, fn)], steps, warmup)
+
+
+def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
+    """The other BASELINE configs, each timed as graph replays on the GPU (values per call)."""
+    dev, BF = "cuda", torch.bfloat16
+    gen = torch.Generator(device=dev).manual_seed(1)
+    res = {}
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, device=dev, generator=gen) * scale).to(BF)
+
+    inv = (1.0 / (1e7 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 64))).to(dev)
+    qnw, knw = rnd(D, scale=0.3), rnd(D, scale=0.3)
+
+    # cfg 1: prep + decode, one row at KV 1024, 16 layers per step
+    L, nl = 1024, 16
+    kcs = [rnd(HKV, L, D) for _ in range(nl)]
+    vcs = [rnd(HKV, L, D) for _ in range(nl)]
+    proj = rnd(1, HQ * 2 * D + 2 * HKV * D + 8, scale=3.0)
+    qg, k, v = proj[:, :HQ * 2 * D], proj[:, HQ * 2 * D:HQ * 2 * D + HKV * D], proj[:, HQ * 2 * D + HKV * D:HQ * 2 * D + 2 * HKV * D]
+    q = torch.empty(1, HQ * D, dtype=BF, device=dev)
+    out = torch.empty(1, HQ * D, dtype=BF, device=dev)
+    ns = qa.default_splits(L, HKV)
+    po, pml = qa.alloc_partials(1, HQ, ns, dev)
+    pos = torch.tensor([L - 1], dtype=torch.int32, device=dev)
+
+    def cfg1():
+        for kk, vv in zip(kcs, vcs):
+            C.attn_prep(qg, k, v, qnw, knw, inv, pos, q, kk, vv, 1e-6)
+            C.attn_decode(q, kk, vv, pos, qg, po, pml, out)
+    us = time_fn_graph(torch, cfg1, steps, warmup) * 1e3 / nl
+    res["cfg1_prep_decode_1k"] = {"us_per_layer": round(us, 3),
+                                  "GBps": round((alg_bytes_layer(L) + 45056) / (us * 1e3), 1)}
+    del kcs, vcs
+
+    # cfg 3: MTP verify, 5 rows at pos 4096 over 4096 cached + 5 new positions
+    L, n, nl = 4096 + 5, 5, 16
+    kcs = [rnd(HKV, L, D) for _ in range(nl)]
+    vcs = [rnd(HKV, L, D) for _ in range(nl)]
+    q5, qg5 = rnd(n, HQ * D), rnd(n, HQ * 2 * D)
+    out5 = torch.empty(n, HQ * D, dtype=BF, device=dev)
+    ns = qa.default_splits(L, HKV)
+    po5, pml5 = qa.alloc_partials(n, HQ, ns, dev)
+    pos5 = torch.tensor([4096], dtype=torch.int32, device=dev)
+
+    def cfg3():
+        for kk, vv in zip(kcs, vcs):
+            C.attn_decode(q5, kk, vv, pos5, qg5, po5, pml5, out5)
+    us = time_fn_graph(torch, cfg3, steps, warmup) * 1e3 / nl
+    res["cfg3_mtp_verify_5rows_4k"] = {"us_per_layer": round(us, 3),
+                                       "GBps": round(alg_bytes_layer(L, n) / (us * 1e3), 1)}
+    del kcs, vcs
+
+    # cfg 4: KV 131072 (537 MB per layer: two layers rotate past the Infinity Cache), plus the
+    # variant with 1% of key rows scaled by 8
+    L, nl = 131072, 2
+    kcs = [rnd(HKV, L, D) for _ in range(nl)]
+    vcs = [rnd(HKV, L, D) for _ in range(nl)]
+    q1, qg1 = rnd(1, HQ * D), rnd(1, HQ * 2 * D)
+    ns = qa.default_splits(L, HKV)
+    po1, pml1 = qa.alloc_partials(1, HQ, ns, dev)
+    pos1 = torch.tensor([L - 1], dtype=torch.int32, device=dev)
+    for name in ("cfg4_long_128k", "cfg4_long_128k_keys_x8"):
+        if name.endswith("x8"):
+            idx = torch.randperm(L, device=dev, generator=gen)[: L // 100]
+            for kk in kcs:
+                kk[:, idx] = (kk[:, idx].float() * 8).to(BF)
+
+        def cfg4():
+            for kk, vv in zip(kcs, vcs):
+                C.attn_decode(q1, kk, vv, pos1, qg1, po1, pml1, out)
+        us = time_fn_graph(torch, cfg4, steps, warmup) * 1e3 / nl
+        res[name] = {"us_per_layer": round(us, 3), "GBps": round(alg_bytes_layer(L) / (us * 1e3), 1),
+                     "hbm_frac": round(alg_bytes_layer(L) / (us * 1e3) / HBM_PEAK_GBS, 4)}
+    del kcs, vcs
+
+    # cfg 5: chunked prefill, 2048 rows appended to a 2048-position cache
+    T, pos0 = 2048, 2048
+    L = pos0 + T
+    kc, vc = rnd(HKV, L, D), rnd(HKV, L, D)
+    projT = rnd(T, HQ * 2 * D + 2 * HKV * D, scale=3.0)
+    qgT, kT, vT = projT[:, :HQ * 2 * D], projT[:, HQ * 2 * D:HQ * 2 * D + HKV * D], projT[:, HQ * 2 * D + HKV * D:]
+    qT = torch.empty(T, HQ * D, dtype=BF, device=dev)
+    outT = torch.empty(T, HQ * D, dtype=BF, device=dev)
+    posT = torch.tensor([pos0], dtype=torch.int32, device=dev)
+    C.attn_prep_chunk(qgT, kT, vT, qnw, knw, inv, posT, qT, kc, vc, 1e-6)
+    flops = 4 * D * HQ * sum(pos0 + 1 + t for t in range(T))
+    ms_attn = time_fn_graph(torch, lambda: C.attn_prefill(qT, kc, vc, posT, qgT, outT), steps, warmup)
+
+    def full():
+        C.attn_prep_chunk(qgT, kT, vT, qnw, knw, inv, posT, qT, kc, vc, 1e-6)
+        C.attn_prefill(qT, kc, vc, posT, qgT, outT)
+    ms_full = time_fn_graph(torch, full, steps, warmup)
+    tflops = flops / (ms_attn * 1e-3) / 1e12
+    res["cfg5_prefill_2048_on_2048"] = {
+        "us_attention": round(ms_attn * 1e3, 2), "us_prep_plus_attention": round(ms_full * 1e3, 2),
+        "GFLOP": round(flops / 1e9, 2), "TFLOPs": round(tflops, 1),
+        "mfma_frac_of_2500_TFLOPs_bf16_dense": round(tflops / 2500.0, 4)}
+    return res
+
+
 def cpu_baseline(torch, L: int, reps: int = 5, warm: int = 2):
     """The reference's PyTorch attention path (reference.py:263-272, restated op for op in
     oracle/) timed on this host's CPU cores: one layer-call at KV length L."""
@@ -186,6 +290,8 @@ def main():
     ap.add_argument("--lengths", default="4096,16384,32768")
     ap.add_argument("--ns", type=int, default=0, help="split count (0 = default policy)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other BASELINE configs (1, 3, 4, 5)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (reads MIB, writes MIB): the "
                          "reference kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE to bytes")
@@ -222,6 +328,11 @@ def main():
               f"({100 * r['partials_frac']:.1f}%)", file=sys.stderr, flush=True)
         sweep.append(r)
     head = next(r for r in sweep if r["L"] == HEADLINE_L)
+    configs = None
+    if not args.no_configs:
+        configs = bench_configs(torch, C, qa, args.steps, args.warmup)
+        for k, v in configs.items():
+            print(f"# {k}: {v}", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu:
@@ -258,6 +369,7 @@ def main():
                      "alg_bytes_per_launch": alg_bytes_partials(HEADLINE_L),
                      "avg_launch_us": round(head["partials_us"], 3)},
         "cpu_baseline": cpu,
+        "configs": configs,
         "sweep": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
                   for r in sweep],
     }

@@ -31,8 +31,8 @@ extern "C" {
 
 /* q/k RMSNorm1p (eps, weights qnw/knw, one bf16 rounding) + partial rotate-half RoPE on the first
  * rd = 2*len(inv_freq) dims (fp32 angle pos*inv_freq, bf16 cos/sin, every op rounded to bf16).
- * Writes q_out[t], and kc/vc[h][pos+t] when pos+t < max_len. Valid: n >= 1, Hq % Hkv == 0,
- * 0 < rd <= 256, rd even, ldp % 8 == 0.
+ * Writes q_out[t], and kc/vc[h][pos+t] when 0 <= pos+t < max_len. Valid: 1 <= n <= 65535,
+ * 0 <= rd <= 256, rd even.
  * Replaces launch_attn_prep (reference csrc/ops.h:25-27, csrc/attn.cu:157-163). */
 hipError_t qe_attn_prep(const void* qg, const void* k, const void* v, long ldp, const void* qnw,
                         const void* knw, const float* inv_freq, const int* pos, void* q_out,
@@ -44,7 +44,7 @@ hipError_t qe_attn_prep(const void* qg, const void* k, const void* v, long ldp, 
  * Two launches: split-KV partials over fixed slices of qe_attn_split_size(max_len, NS)
  * positions, then a log-sum-exp combine with the fused sigmoid gate. Row t of an n-row call is
  * bit-identical to a 1-row call at position pos+t. Valid: 1 <= n <= 8, Hq % Hkv == 0,
- * (Hq/Hkv)*n <= 64, NS >= 1, max_len*512 < 2^32, 16-byte aligned q/kc/vc.
+ * (Hq/Hkv)*n <= 64, NS >= 1, (max_len+32)*512 < 2^32, 16-byte aligned q/kc/vc/part_o.
  * Replaces launch_attn_decode (reference csrc/ops.h:28-30, csrc/attn.cu:165-172). */
 hipError_t qe_attn_decode(const void* q, const void* kc, const void* vc, const int* pos,
                           const void* qg, long ldp, float* part_o, float* part_ml, void* out,
@@ -65,6 +65,18 @@ hipError_t qe_attn_decode_partials(const void* q, const void* kc, const void* vc
 hipError_t qe_attn_decode_combine(const float* part_o, const float* part_ml, const int* pos,
                                   const void* qg, long ldp, void* out, long ldo, int n, int Hq,
                                   int max_len, int NS, hipStream_t stream);
+
+/* Chunked-prefill gated attention: T rows at positions pos..pos+T-1 (q normed and roped, e.g.
+ * by qe_attn_prep with n = T; their K/V already in the cache), row t attends cache positions
+ * [0, min(pos+t+1, max_len)), out[t] = bf16(bf16(softmax . V) * bf16(sigmoid(gate))) with the
+ * gate in qg[t][h][D:2D]. MFMA flash attention with LDS-staged K/V tiles.
+ * Valid: T >= 1, Hq % Hkv == 0, 16-byte aligned q/kc/vc/qg/out, ldp % 8 == 0, ldo % 8 == 0,
+ * (max_len+96)*512 < 2^32. q rows are contiguous ([T][Hq*D]).
+ * No counterpart in the reference: it feeds prompts through the n <= 8 decode path
+ * (python/qengine/engine.py:542-573). */
+hipError_t qe_attn_prefill(const void* q, const void* kc, const void* vc, const int* pos,
+                           const void* qg, long ldp, void* out, long ldo, int T, int Hq, int Hkv,
+                           int max_len, float scale, hipStream_t stream);
 
 /* Number of cache positions per split-KV slice for a cache of max_len positions and NS partial
  * slots: a multiple of 32, at least ceil(max_len/NS). It depends only on (max_len, NS), so the

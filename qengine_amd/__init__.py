@@ -24,7 +24,9 @@ from ._C import (  # noqa: E402,F401
     attn_decode,
     attn_decode_combine,
     attn_decode_partials,
+    attn_prefill,
     attn_prep,
+    attn_prep_chunk,
     set_pdl_launch,
     set_pdl_trigger,
     split_size,

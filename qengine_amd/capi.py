@@ -24,6 +24,7 @@ SIGNATURES = {
     "qe_attn_decode": (_I, [_P, _P, _P, _P, _P, _L, _P, _P, _P, _L, _I, _I, _I, _I, _I, _F, _P]),
     "qe_attn_decode_partials": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P]),
     "qe_attn_decode_combine": (_I, [_P, _P, _P, _P, _L, _P, _L, _I, _I, _I, _I, _P]),
+    "qe_attn_prefill": (_I, [_P, _P, _P, _P, _P, _L, _P, _L, _I, _I, _I, _I, _F, _P]),
     "qe_attn_split_size": (_I, [_I, _I]),
     "qe_attn_version": (ctypes.c_char_p, []),
     "qe_set_pdl_trigger": (None, [_I]),
@@ -88,6 +89,12 @@ def decode_combine(part_o, part_ml, pos, qg, ldp, out, ldo, n, hq, max_len, ns,
                    stream=None) -> int:
     return load().qe_attn_decode_combine(_ptr(part_o), _ptr(part_ml), _ptr(pos), _ptr(qg), ldp,
                                          _ptr(out), ldo, n, hq, max_len, ns, _stream(stream))
+
+
+def prefill(q, kc, vc, pos, qg, ldp, out, ldo, T, hq, hkv, max_len, scale=1.0 / 16,
+            stream=None) -> int:
+    return load().qe_attn_prefill(_ptr(q), _ptr(kc), _ptr(vc), _ptr(pos), _ptr(qg), ldp, _ptr(out),
+                                  ldo, T, hq, hkv, max_len, scale, _stream(stream))
 
 
 def split_size(max_len: int, ns: int) -> int:

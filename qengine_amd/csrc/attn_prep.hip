@@ -41,7 +41,11 @@ attn_prep_kernel(const __bf16* __restrict__ qg, const __bf16* __restrict__ k,
   if (c < rd) {
     const int half = rd >> 1;
     const float ang = (float)pos * inv_freq[c < half ? c : c - half];  // fp32 angle
-    const float cs = round_bf16(cosf(ang)), sn = round_bf16(sinf(ang));
+    // cos/sin of the fp32 angle evaluated in fp64 and rounded once: the correctly rounded fp32
+    // value, which is what the reference's fp32 cos/sin return in all but rare cases (single
+    // precision device cos/sin can be a couple of ulps off, enough to flip a bf16 rounding).
+    const double angd = (double)ang;
+    const float cs = round_bf16((float)cos(angd)), sn = round_bf16((float)sin(angd));
     const float rot = c < half ? -xn[c + half] : xn[c - half];  // rotate_half
     y = round_bf16(round_bf16(xv * cs) + round_bf16(rot * sn));
   }

@@ -70,7 +70,7 @@ PrepArgs parse_prep(const torch::Tensor& qg, const torch::Tensor& k, const torch
                     const torch::Tensor& qnw, const torch::Tensor& knw,
                     const torch::Tensor& inv_freq, const torch::Tensor& pos,
                     const torch::Tensor& q_out, const torch::Tensor& kc, const torch::Tensor& vc,
-                    bool dev) {
+                    bool dev, int max_rows = 8) {
   auto QG = rows(qg, BF, "qg", dev), K = rows(k, BF, "k", dev), V = rows(v, BF, "v", dev);
   auto QO = rows(q_out, BF, "q_out", dev);
   TORCH_CHECK(QG.ld == K.ld && QG.ld == V.ld, "qg/k/v must share a row stride");
@@ -82,8 +82,8 @@ PrepArgs parse_prep(const torch::Tensor& qg, const torch::Tensor& k, const torch
   chk_pos(pos, dev);
   TORCH_CHECK(kc.dim() == 3 && kc.size(2) == HD, "head_dim 256 only");
   const int n = QG.n, Hkv = kc.size(0), max_len = kc.size(1), Hq = QO.w / HD;
-  TORCH_CHECK(n >= 1 && n <= 8 && K.n == n && V.n == n && QO.n == n && QO.ld == QO.w,
-              "prep takes 1..8 rows, equal in every argument, and contiguous q_out rows");
+  TORCH_CHECK(n >= 1 && n <= max_rows && K.n == n && V.n == n && QO.n == n && QO.ld == QO.w,
+              "prep takes 1..", max_rows, " rows, equal in every argument, and contiguous q_out rows");
   TORCH_CHECK(Hq >= 1 && QG.w == (long)Hq * 2 * HD && K.w == (long)Hkv * HD &&
                   V.w == (long)Hkv * HD,
               "row widths must be qg = Hq*512, k = v = Hkv*256");
@@ -142,6 +142,45 @@ void attn_prep(torch::Tensor qg, torch::Tensor k, torch::Tensor v, torch::Tensor
                         q_out.data_ptr(), kc.data_ptr(), vc.data_ptr(), a.n, a.Hq, a.Hkv,
                         a.max_len, a.rd, (float)eps, stream_of(qg)),
            "qe_attn_prep");
+}
+
+// attn_prep for a prefill chunk: the same op without the 8-row limit (rows up to 65535).
+void attn_prep_chunk(torch::Tensor qg, torch::Tensor k, torch::Tensor v, torch::Tensor qnw,
+                     torch::Tensor knw, torch::Tensor inv_freq, torch::Tensor pos,
+                     torch::Tensor q_out, torch::Tensor kc, torch::Tensor vc, double eps) {
+  const auto a = parse_prep(qg, k, v, qnw, knw, inv_freq, pos, q_out, kc, vc, true, 65535);
+  const c10::DeviceGuard guard(qg.device());
+  raise_on(qe_attn_prep(qg.data_ptr(), k.data_ptr(), v.data_ptr(), a.ldp, qnw.data_ptr(),
+                        knw.data_ptr(), inv_freq.data_ptr<float>(), pos.data_ptr<int>(),
+                        q_out.data_ptr(), kc.data_ptr(), vc.data_ptr(), a.n, a.Hq, a.Hkv,
+                        a.max_len, a.rd, (float)eps, stream_of(qg)),
+           "qe_attn_prep");
+}
+
+// Chunked prefill: q [T, Hq*256] contiguous (normed + roped), kc/vc [Hkv, max_len, 256] holding
+// the chunk's K/V, qg rows [T, >= Hq*512] (gate source), out rows [T, Hq*256].
+void attn_prefill(torch::Tensor q, torch::Tensor kc, torch::Tensor vc, torch::Tensor pos,
+                  torch::Tensor qg, torch::Tensor out) {
+  auto Qr = rows(q, BF, "q", true), QG = rows(qg, BF, "qg", true), O = rows(out, BF, "out", true);
+  chk(kc, BF, "kc", true);
+  chk(vc, BF, "vc", true);
+  chk_pos(pos, true);
+  chk16(q, Qr.ld, "q");
+  chk16(qg, QG.ld, "qg");
+  chk16(out, O.ld, "out");
+  chk16(kc, HD, "kc");
+  chk16(vc, HD, "vc");
+  TORCH_CHECK(kc.dim() == 3 && kc.size(2) == HD && vc.sizes() == kc.sizes(),
+              "kc/vc must be [Hkv, max_len, 256] with equal sizes");
+  const int T = Qr.n, Hq = Qr.w / HD, Hkv = kc.size(0), max_len = kc.size(1);
+  TORCH_CHECK(Hq >= 1 && Qr.ld == Qr.w && QG.n == T && O.n == T && Hq % Hkv == 0,
+              "q rows must be contiguous, rows must agree and Hq % Hkv == 0");
+  TORCH_CHECK(O.w == (long)Hq * HD && QG.w >= (long)Hq * 2 * HD, "out width Hq*256; qg width Hq*512");
+  const c10::DeviceGuard guard(q.device());
+  raise_on(qe_attn_prefill(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), pos.data_ptr<int>(),
+                           qg.data_ptr(), QG.ld, out.data_ptr(), O.ld, T, Hq, Hkv, max_len,
+                           1.0f / 16.0f, stream_of(q)),
+           "qe_attn_prefill");
 }
 
 // q: [n, Hq*256] contiguous; part_o: fp32 [>=n, Hq, NS, 256]; part_ml: [>=n, Hq, NS, 2];
@@ -204,6 +243,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "split-KV partials of attn_decode (same arguments)");
   m.def("attn_decode_combine", &attn_decode_combine,
         "log-sum-exp combine + sigmoid gate of attn_decode (same arguments)");
+  m.def("attn_prep_chunk", &attn_prep_chunk, "attn_prep without the 8-row limit (prefill chunks)");
+  m.def("attn_prefill", &attn_prefill,
+        "chunked-prefill gated attention over the KV cache (q, kc, vc, pos, qg, out)");
   m.def("split_size", [](int max_len, int NS) { return qe_attn_split_size(max_len, NS); },
         "cache positions per split-KV slice for (max_len, NS)");
   m.def("version", []() { return std::string(qe_attn_version()); });

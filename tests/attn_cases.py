@@ -117,3 +117,25 @@ def attn_close(out: torch.Tensor, ref: torch.Tensor):
     ok = bool((d <= 2.0 ** -6 * r.abs() + 2e-3).all())
     mx, mean = d.max().item(), d.mean().item()
     return ok and mx <= 2e-2 and mean <= 2e-3, mx, mean
+
+
+def rope_close(a: torch.Tensor, ref: torch.Tensor, rd: int = 64, exact_frac: float = 0.999):
+    """Prep outputs (q rows or cache rows, last dim a multiple of 256) against the oracle.
+    Dims >= rd (not rotated): within 1 bf16 ulp. Rotated dims: within 2 ulps of the pair
+    magnitude max(|y_c|, |y_partner|). A rotation keeps each pair's norm, while a 1-ulp flip of
+    the normed input (fp32 summation order of the RMS) moves y by up to one ulp of the larger
+    term, which is many ulps of y itself when the two rotated terms cancel. Also requires
+    exact_frac of all elements to be bit-equal. Returns (ok, max diff, exact fraction)."""
+    a = a.float().reshape(-1, D)
+    r = ref.float().reshape(-1, D)
+    half = rd // 2
+    partner = torch.cat([r[:, half:rd], r[:, :half]], dim=1)
+    mag = torch.cat([torch.maximum(r[:, :rd].abs(), partner.abs()), r[:, rd:].abs()], dim=1)
+    mag = torch.maximum(mag, a.abs())
+    spacing = torch.exp2(torch.floor(torch.log2(mag.clamp_min(1e-30))) - 7)
+    ulps = torch.ones_like(spacing)
+    ulps[:, :rd] = 2
+    d = (a - r).abs()
+    ok = bool((d <= ulps * spacing).all())
+    frac = (a == r).float().mean().item()
+    return ok and frac >= exact_frac, d.max().item(), frac
