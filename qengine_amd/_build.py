@@ -25,6 +25,10 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["attn_prep.hip", "attn_decode.hip", "attn_prefill.hip"]
+# Per-source code-generation flags. The prefill tile loop keeps 128 fp32 accumulators live; the
+# compiler's default MFMA register form parks them in AGPRs and copies all of them into VGPRs
+# on every iteration. The VGPR form keeps them in place.
+SOURCE_FLAGS = {"attn_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 LIB = PKG / "libqe_attn.so"
 EXT = PKG / ("_C" + sysconfig.get_config_var("EXT_SUFFIX"))
 
@@ -51,7 +55,8 @@ def _hip_objects() -> list[Path]:
     srcs = [CSRC / s for s in HIP_SOURCES if (CSRC / s).exists()]
     objs = [OBJ / (s.stem + ".o") for s in srcs]
     with ThreadPoolExecutor(max_workers=min(4, len(srcs))) as ex:
-        list(ex.map(lambda so: _run([HIPCC, *HIP_FLAGS, "-c", str(so[0]), "-o", str(so[1])]),
+        list(ex.map(lambda so: _run([HIPCC, *HIP_FLAGS, *SOURCE_FLAGS.get(so[0].name, []), "-c",
+                                     str(so[0]), "-o", str(so[1])]),
                     zip(srcs, objs)))
     return objs
 

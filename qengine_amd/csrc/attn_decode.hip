@@ -23,7 +23,7 @@
 //    moved (an exact no-op).
 //  * Buffer resources bound the K/V reads to the slice: positions past it load as 0.
 //  * A second launch merges the slices (log-sum-exp) and applies the sigmoid gate.
-#include "qe_device.hpp"
+#include "attn_tile.hpp"
 #include "qe_attn.h"
 
 namespace qe {
@@ -35,7 +35,7 @@ constexpr int TILE = 32;               // cache positions per wave step (two 16-
 // a 1-row call. (Eight waves for NT = 1 were measured no faster on MI355X.)
 template <int NT>
 constexpr int waves_for() { return 4; }
-constexpr int ROW_CHUNKS = HD * 2 / 16;  // 16-byte chunks per cache row (32)
+using tile::ROW_CHUNKS;
 
 __host__ __device__ inline int split_size(int max_len, int NS) {
   long per = ((long)max_len + NS - 1) / NS;
@@ -47,10 +47,6 @@ __host__ __device__ inline int split_size(int max_len, int NS) {
 struct VTile {
   u32x4_t v[8][2];  // V rows P(g4, e) = p0 + 16(e>>2) + 4g4 + (e&3), dims 128h + 8c + [0, 8)
 };
-
-// LDS slot of (row r, chunk q) in a wave's K tile: chunks are XOR-swizzled by r & 15, so the
-// 16 lanes that read one chunk column of 16 different rows hit 16 different bank groups.
-__device__ __forceinline__ int k_slot(int r, int q) { return r * ROW_CHUNKS + (q ^ (r & 15)); }
 
 // Issue one tile's loads: 16 LDS-DMA loads of K (instruction j covers rows 2j, 2j+1: lane i
 // fetches the chunk that belongs in LDS slot 64j + i, so each instruction reads 1 KB of
@@ -72,95 +68,6 @@ __device__ __forceinline__ void load_tile(VTile& b, u32x4_t* ks_lds, __amdgpu_bu
           vrs, (uint32_t)(p0 + 16 * (e >> 2) + 4 * g4 + (e & 3)) * (HD * 2) + (128 * h + 8 * c) * 2);
 }
 
-// Scores, online softmax and P.V for one tile whose K rows are in the wave's LDS tile `ks_lds`.
-// Column state: running max m (log2 units), running sum l (this lane's 8 positions per tile; the
-// 4 lane groups are summed at the end) and the O^T accumulators acc[ct][h][i] (rows = dims
-// 128h + 32g4 + 8ii + i of column c).
-template <int NT>
-__device__ __forceinline__ void compute_tile(const VTile& b, const u32x4_t* ks_lds, int p0,
-                                             const int (&Lcol)[NT], const bf16x8_t (&qb)[NT][8],
-                                             float scale_log2, int c, int g4, float (&m)[NT],
-                                             float (&l)[NT], f32x4_t (&acc)[NT][2][8]) {
-  // S^T = K Q^T: A operand row c of M-tile T is position p0 + 16T + c, k-step ks holds dims
-  // [32ks + 8g4, +8). Lane holds positions p0 + 16T + 4g4 + i of column c.
-  f32x4_t sacc[NT][2];
-#pragma unroll
-  for (int T = 0; T < 2; ++T) {
-#pragma unroll
-    for (int ct = 0; ct < NT; ++ct) sacc[ct][T] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      const bf16x8_t kop = as_bf16x8(ks_lds[k_slot(16 * T + c, 4 * ks + g4)]);
-#pragma unroll
-      for (int ct = 0; ct < NT; ++ct) sacc[ct][T] = mfma16x16x32(kop, qb[ct][ks], sacc[ct][T]);
-    }
-  }
-
-  // Online softmax per column (log2 domain). P^T goes to the B operand with element e <-> P(g4, e),
-  // as two bf16 terms hi + lo (hi = bf16(p), lo = bf16(p - hi)): ~2^-17 relative error, so P.V
-  // keeps fp32-class accuracy at the cost of a second MFMA per tile.
-  float corr[NT];
-  u32x4_t pb_hi[NT], pb_lo[NT];
-  bool moved = false;
-#pragma unroll
-  for (int ct = 0; ct < NT; ++ct) {
-    float sv[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int p = p0 + 16 * (e >> 2) + 4 * g4 + (e & 3);
-      const float x = sacc[ct][e >> 2][e & 3] * scale_log2;
-      sv[e] = p < Lcol[ct] ? x : -INFINITY;
-    }
-    float tmax = sv[0];
-#pragma unroll
-    for (int e = 1; e < 8; ++e) tmax = fmaxf(tmax, sv[e]);
-    tmax = group4_max(tmax);
-    const float mnew = fmaxf(m[ct], tmax);
-    const float msub = mnew == -INFINITY ? 0.f : mnew;
-    corr[ct] = mnew == m[ct] ? 1.f : __builtin_amdgcn_exp2f(m[ct] - msub);
-    moved |= corr[ct] != 1.f;
-    float pf[8], plo[8];
-    float lsum = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      pf[e] = __builtin_amdgcn_exp2f(sv[e] - msub);
-      lsum += pf[e];
-      plo[e] = pf[e] - round_bf16(pf[e]);
-    }
-    l[ct] = l[ct] * corr[ct] + lsum;
-    m[ct] = mnew;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      pb_hi[ct][d] = pack_bf16x2(pf[2 * d], pf[2 * d + 1]);
-      pb_lo[ct][d] = pack_bf16x2(plo[2 * d], plo[2 * d + 1]);
-    }
-  }
-  if (__any(moved)) {  // exact no-op when no column's max moved, so skipped
-#pragma unroll
-    for (int ct = 0; ct < NT; ++ct)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[ct][h][i] *= corr[ct];
-  }
-
-  // O^T += V^T P^T. A-operand row c of tile (h, i) is dim 128h + 8c + i over the 8 positions.
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      u32x4_t a;
-#pragma unroll
-      for (int d = 0; d < 4; ++d)
-        a[d] = interleave_halves(b.v[2 * d][h][i >> 1], b.v[2 * d + 1][h][i >> 1], i & 1);
-#pragma unroll
-      for (int ct = 0; ct < NT; ++ct) {
-        acc[ct][h][i] = mfma16x16x32(as_bf16x8(a), as_bf16x8(pb_hi[ct]), acc[ct][h][i]);
-        acc[ct][h][i] = mfma16x16x32(as_bf16x8(a), as_bf16x8(pb_lo[ct]), acc[ct][h][i]);
-      }
-    }
-}
-
 // Order this wave's LDS accesses: the compiler must not move LDS reads/writes across it (lanes
 // exchange data through LDS, which single-thread alias analysis cannot see).
 __device__ __forceinline__ void wave_lds_fence() {
@@ -169,17 +76,31 @@ __device__ __forceinline__ void wave_lds_fence() {
 }
 
 // Wait for the tile's K (its 16 LDS-DMA loads were issued before the 16 V loads, so at most 16
-// loads may remain in flight), then compute the tile.
+// loads may remain in flight), then compute the tile. Masking is needed only on tiles reaching
+// past the shortest attended length among the real columns (Lmin).
 template <int NT>
 __device__ __forceinline__ void wait_and_compute(const VTile& b, const u32x4_t* ks_lds, int p0,
-                                                 const int (&Lcol)[NT],
+                                                 int Lmin, const int (&Lcol)[NT],
                                                  const bf16x8_t (&qb)[NT][8], float scale_log2,
                                                  int c, int g4, float (&m)[NT], float (&l)[NT],
                                                  f32x4_t (&acc)[NT][2][8]) {
   vmcnt_wait<16>();
   wave_lds_fence();
-  compute_tile<NT>(b, ks_lds, p0, Lcol, qb, scale_log2, c, g4, m, l, acc);
+  f32x4_t sacc[NT][2];
+  tile::qk_tile<NT>(ks_lds, qb, c, g4, sacc);
   wave_lds_fence();  // this tile's K reads happen before the next tile's LDS-DMA writes
+  u32x4_t pb_hi[NT], pb_lo[NT];
+  if (p0 + TILE > Lmin)
+    tile::softmax_tile<NT, true, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
+  else
+    tile::softmax_tile<NT, false, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    u32x4_t vr[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vr[e] = b.v[e][hh];
+    tile::pv_half<NT, true>(vr, hh, pb_hi, pb_lo, acc);
+  }
 }
 
 // LDS: per-wave K tiles during the loop; reused for the cross-wave merge afterwards.
@@ -233,6 +154,7 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc
     }
   }
 
+  const int Lmin = min(pos0 + 1, max_len);  // row 0 attends the fewest positions
   const size_t head_off = (size_t)g * max_len * HD;
   const uint32_t bytes = (uint32_t)end * (uint32_t)(HD * 2);  // loads past the slice read 0
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(kc + head_off, bytes);
@@ -253,7 +175,7 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc
   for (int p0 = beg + w * TILE; p0 < end; p0 += WAVES * TILE) {
     VTile buf;
     load_tile(buf, ks_lds, krs, vrs, p0, lane, c, g4);
-    wait_and_compute<NT>(buf, ks_lds, p0, Lcol, qb, scale_log2, c, g4, m, l, acc);
+    wait_and_compute<NT>(buf, ks_lds, p0, Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
   }
 
   // ---- merge the waves of this workgroup in a fixed order and write the slice's partial

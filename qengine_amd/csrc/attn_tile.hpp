@@ -1,0 +1,130 @@
+// One 32-position tile of gated attention on MFMA, shared by the decode and prefill kernels.
+//
+// Layout (wave64, v_mfma_f32_16x16x32_bf16, lane = 16*g4 + c):
+//  * Columns are queries (q head x row); a wave holds NT column tiles of 16 in registers as the
+//    B operand qb[ct][ks] (dims [32ks + 8g4, +8) of column ct*16 + c).
+//  * S^T = K Q^T: the A operand (16 positions x 32 dims) is read from the wave's or workgroup's
+//    LDS K tile (XOR-swizzled, see k_slot). Lane holds positions p0 + 16T + 4g4 + i of column c.
+//  * O^T += V^T P^T: P^T is the B operand with element e <-> position P(g4, e) = p0 + 16(e>>2) +
+//    4g4 + (e&3); V^T's A operand row c of M-tile (hh, i) is dim 128hh + 8c + i, built by v_perm
+//    from 16-byte pieces of 8 positions. Accumulator acc[ct][hh][i][ii] = O^T[dim 128hh + 32g4 +
+//    8ii + i][column c].
+//  * Online softmax per column in the log2 domain with lazy rescaling: a column's reference max
+//    only moves when a score exceeds it by more than LAZY_TAU, so p = exp2(s - m_ref) <= 2^TAU
+//    and the accumulators are rescaled rarely. O/L is unchanged mathematically, and each column's
+//    arithmetic depends on that column alone.
+#pragma once
+#include "qe_device.hpp"
+
+namespace qe {
+namespace tile {
+
+constexpr int BN = 32;                   // positions per tile (two 16-row MFMA tiles)
+constexpr int ROW_CHUNKS = HD * 2 / 16;  // 16-byte chunks per 512-byte cache row
+constexpr float LAZY_TAU = 8.f;          // log2 headroom before the reference max must move
+
+// LDS slot of (row r, chunk q) in a K tile: chunks XOR-swizzled by r & 15, so the 16 lanes that
+// read one chunk column of 16 rows hit 16 different bank groups.
+__device__ __forceinline__ int k_slot(int r, int q) { return r * ROW_CHUNKS + (q ^ (r & 15)); }
+
+// S^T for one tile: sacc[ct][T] holds positions p0 + 16T + 4g4 + i of column ct*16 + c.
+template <int NT>
+__device__ __forceinline__ void qk_tile(const u32x4_t* k_lds, const bf16x8_t (&qb)[NT][8], int c,
+                                        int g4, f32x4_t (&sacc)[NT][2]) {
+#pragma unroll
+  for (int T = 0; T < 2; ++T) {
+#pragma unroll
+    for (int ct = 0; ct < NT; ++ct) sacc[ct][T] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const bf16x8_t kop = as_bf16x8(k_lds[k_slot(16 * T + c, 4 * ks + g4)]);
+#pragma unroll
+      for (int ct = 0; ct < NT; ++ct) sacc[ct][T] = mfma16x16x32(kop, qb[ct][ks], sacc[ct][T]);
+    }
+  }
+}
+
+// Online softmax of one tile. MASK: positions >= Lcol[ct] are excluded (needed only on tiles that
+// reach past the shortest attended length among the real columns). SPLIT: P goes to the PV MFMA
+// as bf16 hi + lo terms (~2^-17 relative) instead of one bf16 term (2^-9).
+template <int NT, bool MASK, bool SPLIT>
+__device__ __forceinline__ void softmax_tile(const f32x4_t (&sacc)[NT][2], int p0,
+                                             const int (&Lcol)[NT], float scale_log2, int g4,
+                                             float (&m)[NT], float (&l)[NT],
+                                             f32x4_t (&acc)[NT][2][8], u32x4_t (&pb_hi)[NT],
+                                             u32x4_t (&pb_lo)[NT]) {
+  float corr[NT];
+  bool moved = false;
+#pragma unroll
+  for (int ct = 0; ct < NT; ++ct) {
+    float sv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = sacc[ct][e >> 2][e & 3] * scale_log2;
+      if constexpr (MASK) {
+        const int p = p0 + 16 * (e >> 2) + 4 * g4 + (e & 3);
+        sv[e] = p < Lcol[ct] ? x : -INFINITY;
+      } else {
+        sv[e] = x;
+      }
+    }
+    float tmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                       fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+    tmax = group4_max(tmax);
+    corr[ct] = 1.f;
+    if (tmax > m[ct] + LAZY_TAU) {  // also taken on the first finite tile (m = -inf)
+      if (m[ct] != -INFINITY) {
+        corr[ct] = __builtin_amdgcn_exp2f(m[ct] - tmax);
+        moved = true;
+      }
+      m[ct] = tmax;
+    }
+    const float msub = m[ct] == -INFINITY ? 0.f : m[ct];
+    float pf[8];
+    float lsum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      pf[e] = __builtin_amdgcn_exp2f(sv[e] - msub);
+      lsum += pf[e];
+    }
+    l[ct] = l[ct] * corr[ct] + lsum;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) pb_hi[ct][d] = pack_bf16x2(pf[2 * d], pf[2 * d + 1]);
+    if constexpr (SPLIT) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        pb_lo[ct][d] = pack_bf16x2(pf[2 * d] - lo_bf16(pb_hi[ct][d]),
+                                   pf[2 * d + 1] - hi_bf16(pb_hi[ct][d]));
+    }
+  }
+  if (__any(moved)) {  // a multiply by exactly 1 for columns that did not move
+#pragma unroll
+    for (int ct = 0; ct < NT; ++ct)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[ct][hh][i] *= corr[ct];
+  }
+}
+
+// O^T += V^T P^T for dims [128hh, 128hh + 128): vr[e] = 16 bytes of V row P(g4, e), dims
+// 128hh + 8c + [0, 8).
+template <int NT, bool SPLIT>
+__device__ __forceinline__ void pv_half(const u32x4_t (&vr)[8], int hh, const u32x4_t (&pb_hi)[NT],
+                                        const u32x4_t (&pb_lo)[NT], f32x4_t (&acc)[NT][2][8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    u32x4_t a;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) a[d] = interleave_halves(vr[2 * d][i >> 1], vr[2 * d + 1][i >> 1], i & 1);
+#pragma unroll
+    for (int ct = 0; ct < NT; ++ct) {
+      acc[ct][hh][i] = mfma16x16x32(as_bf16x8(a), as_bf16x8(pb_hi[ct]), acc[ct][hh][i]);
+      if constexpr (SPLIT)
+        acc[ct][hh][i] = mfma16x16x32(as_bf16x8(a), as_bf16x8(pb_lo[ct]), acc[ct][hh][i]);
+    }
+  }
+}
+
+}  // namespace tile
+}  // namespace qe
