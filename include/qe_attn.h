@@ -44,7 +44,7 @@ hipError_t qe_attn_prep(const void* qg, const void* k, const void* v, long ldp, 
  * Two launches: split-KV partials over fixed slices of qe_attn_split_size(max_len, NS)
  * positions, then a log-sum-exp combine with the fused sigmoid gate. Row t of an n-row call is
  * bit-identical to a 1-row call at position pos+t. Valid: 1 <= n <= 8, Hq % Hkv == 0,
- * (Hq/Hkv)*n <= 64, NS >= 1, (max_len+32)*512 < 2^32, 16-byte aligned q/kc/vc/part_o.
+ * (Hq/Hkv)*n <= 64, NS >= 1, (max_len+128)*512 < 2^32, 16-byte aligned q/kc/vc/part_o.
  * Replaces launch_attn_decode (reference csrc/ops.h:28-30, csrc/attn.cu:165-172). */
 hipError_t qe_attn_decode(const void* q, const void* kc, const void* vc, const int* pos,
                           const void* qg, long ldp, float* part_o, float* part_ml, void* out,
@@ -71,7 +71,7 @@ hipError_t qe_attn_decode_combine(const float* part_o, const float* part_ml, con
  * [0, min(pos+t+1, max_len)), out[t] = bf16(bf16(softmax . V) * bf16(sigmoid(gate))) with the
  * gate in qg[t][h][D:2D]. MFMA flash attention with LDS-staged K/V tiles.
  * Valid: T >= 1, Hq % Hkv == 0, 16-byte aligned q/kc/vc/qg/out, ldp % 8 == 0, ldo % 8 == 0,
- * (max_len+96)*512 < 2^32. q rows are contiguous ([T][Hq*D]).
+ * (max_len+160)*512 < 2^32. q rows are contiguous ([T][Hq*D]).
  * No counterpart in the reference: it feeds prompts through the n <= 8 decode path
  * (python/qengine/engine.py:542-573). */
 hipError_t qe_attn_prefill(const void* q, const void* kc, const void* vc, const int* pos,

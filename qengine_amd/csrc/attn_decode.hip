@@ -83,7 +83,7 @@ __device__ __forceinline__ void wait_and_compute(const VTile& b, const u32x4_t* 
                                                  int Lmin, const int (&Lcol)[NT],
                                                  const bf16x8_t (&qb)[NT][8], float scale_log2,
                                                  int c, int g4, float (&m)[NT], float (&l)[NT],
-                                                 f32x4_t (&acc)[NT][2][8]) {
+                                                 f32x4_t (&acc)[NT][16]) {
   vmcnt_wait<16>();
   wave_lds_fence();
   f32x4_t sacc[NT][2];
@@ -106,7 +106,6 @@ __device__ __forceinline__ void wait_and_compute(const VTile& b, const u32x4_t* 
 // LDS: per-wave K tiles during the loop; reused for the cross-wave merge afterwards.
 template <int WAVES>
 constexpr int lds_k_bytes() { return WAVES * TILE * HD * 2; }  // 16 KB per wave
-static_assert(4 * 32 * WAVE * 4 <= lds_k_bytes<4>(), "merge buffer aliases the K tiles");
 
 // part_o [n][Hq][NS][HD] (unnormalised O), part_ml [n][Hq][NS][2] = (max in log2 units, sum).
 // NT = 1 (decode, 1-2 rows) fits in 256 registers, which lets two workgroups share a CU (one
@@ -161,15 +160,13 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vc + head_off, bytes);
 
   float m[NT], l[NT];
-  f32x4_t acc[NT][2][8];
+  f32x4_t acc[NT][16];  // [8hh + i]: O^T dims 128hh + 32g4 + 8ii + i (tile::pv_half)
 #pragma unroll
   for (int ct = 0; ct < NT; ++ct) {
     m[ct] = -INFINITY;
     l[ct] = 0.f;
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[ct][h][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int a = 0; a < 16; ++a) acc[ct][a] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
   for (int p0 = beg + w * TILE; p0 < end; p0 += WAVES * TILE) {
@@ -213,37 +210,38 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc
     }
   }
 
-  float (*s_acc)[32][WAVE] = reinterpret_cast<float (*)[32][WAVE]>(lds);
+  // Each wave parks the O^T accumulators of its real columns in LDS as 16-byte rows (lanes of
+  // padding columns stay idle, which keeps the LDS traffic to what the merge needs), one barrier,
+  // then thread (w, lane) merges h = w/2, i in [4(w&1), +4) over waves 0..3 in that order and
+  // writes 4 x 16 bytes: dims 128h + 32g4 + 8ii + 4(w&1) + [0, 4) for ii = 0..3.
+  static_assert(WAVES == 4, "merge layout assumes 4 waves");
+  static_assert(WAVES * 16 * WAVE * 16 <= lds_k_bytes<WAVES>(), "merge buffer aliases the K tiles");
+  f32x4_t (*s_acc)[16][WAVE] = reinterpret_cast<f32x4_t (*)[16][WAVE]>(lds);
 #pragma unroll
   for (int ct = 0; ct < NT; ++ct) {
     const int col = ct * 16 + c;
+    if (ct > 0) __syncthreads();  // the previous column tile's reads are done
+    if (col < ncols) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+      for (int a = 0; a < 16; ++a) s_acc[w][a][lane] = acc[ct][a];
+    }
+    __syncthreads();
+    if (col < ncols) {
+      const int h = w >> 1, i0 = 4 * (w & 1);
+      f32x4_t mo[4];
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int k = 0; k < 4; ++k) {
+        f32x4_t sum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) s_acc[w][i * 4 + ii][lane] = acc[ct][h][i][ii];
-      __syncthreads();
-      // this thread merges ii = w % 4 for VPT consecutive i: dims 128h + 32g4 + 8ii + i
-      constexpr int VPT = 32 / WAVES;
-      const int ii = w & 3, i0 = (w >> 2) * VPT;
-      float o[VPT];
-#pragma unroll
-      for (int k = 0; k < VPT; ++k) {
-        float sum = 0.f;
-#pragma unroll
-        for (int v = 0; v < WAVES; ++v) sum += s_acc[v][(i0 + k) * 4 + ii][lane] * wsc[ct][v];
-        o[k] = sum;
+        for (int v = 0; v < WAVES; ++v) sum += s_acc[v][8 * h + i0 + k][lane] * wsc[ct][v];
+        mo[k] = sum;
       }
-      if (col < ncols) {
-        const int t = col / grp, head = g * grp + (col - t * grp);
-        float* dst =
-            part_o + (((size_t)t * Hq + head) * NS + s) * HD + 128 * h + 32 * g4 + 8 * ii + i0;
+      const int t = col / grp, head = g * grp + (col - t * grp);
+      float* dst = part_o + (((size_t)t * Hq + head) * NS + s) * HD + 128 * h + 32 * g4 + i0;
 #pragma unroll
-        for (int k = 0; k < VPT; k += 4)
-          reinterpret_cast<f32x4_t*>(dst)[k / 4] = f32x4_t{o[k], o[k + 1], o[k + 2], o[k + 3]};
-      }
-      __syncthreads();
+      for (int ii = 0; ii < 4; ++ii)
+        reinterpret_cast<f32x4_t*>(dst + 8 * ii)[0] =
+            f32x4_t{mo[0][ii], mo[1][ii], mo[2][ii], mo[3][ii]};
     }
   }
 }
@@ -301,8 +299,7 @@ attn_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ 
     float bm = M;
 #pragma unroll
     for (int b = 0; b < COMBINE_BATCH; ++b) bm = valid[b] ? fmaxf(bm, mls[b].x) : bm;
-    bm = fmaxf(bm, __shfl_xor(bm, 16));
-    bm = fmaxf(bm, __shfl_xor(bm, 32));
+    bm = group4_max(bm);
     if (bm != M) {  // rescale what was accumulated under the old max (exact no-op otherwise)
       const float r = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - bm);
       O *= r;
@@ -318,12 +315,9 @@ attn_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ 
       }
     }
   }
+  L = group4_sum(L);
 #pragma unroll
-  for (int o = 16; o <= 32; o <<= 1) {
-    L += __shfl_xor(L, o);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) O[i] += __shfl_xor(O[i], o);
-  }
+  for (int i = 0; i < 4; ++i) O[i] = group4_sum(O[i]);
   if (sg == 0) {
     __bf16* op = out + (size_t)t * ldo + (size_t)h * HD + dim;
 #pragma unroll

@@ -60,7 +60,7 @@ __device__ __forceinline__ void issue_tile(u32x4_t* stage, __amdgpu_buffer_rsrc_
 // Per-wave running softmax state and O^T accumulators.
 struct WaveState {
   float m[NT], l[NT];
-  f32x4_t acc[NT][2][8];
+  f32x4_t acc[NT][16];  // [8hh + i]: see tile::pv_half
 };
 
 // Tiles [j0, j1) of the ring with one branch-free body (SPLIT and MASK fixed).
@@ -149,9 +149,7 @@ attn_prefill_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
     st.m[ct] = -INFINITY;
     st.l[ct] = 0.f;
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) st.acc[ct][hh][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int a = 0; a < 16; ++a) st.acc[ct][a] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
   // Ring of STAGES tiles, AHEAD in flight. One barrier per tile: after the barrier of tile j every
@@ -186,8 +184,8 @@ attn_prefill_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
         u32x4_t ob;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          const float o0 = round_bf16(st.acc[ct][hh][2 * k][ii] / L);
-          const float o1 = round_bf16(st.acc[ct][hh][2 * k + 1][ii] / L);
+          const float o0 = round_bf16(st.acc[ct][8 * hh + 2 * k][ii] / L);
+          const float o1 = round_bf16(st.acc[ct][8 * hh + 2 * k + 1][ii] / L);
           const float s0 = round_bf16(sigmoid_f32(lo_bf16(gb[k])));
           const float s1 = round_bf16(sigmoid_f32(hi_bf16(gb[k])));
           ob[k] = pack_bf16x2(o0 * s0, o1 * s1);

@@ -6,9 +6,8 @@
 //  * S^T = K Q^T: the A operand (16 positions x 32 dims) is read from the wave's or workgroup's
 //    LDS K tile (XOR-swizzled, see k_slot). Lane holds positions p0 + 16T + 4g4 + i of column c.
 //  * O^T += V^T P^T: P^T is the B operand with element e <-> position P(g4, e) = p0 + 16(e>>2) +
-//    4g4 + (e&3); V^T's A operand row c of M-tile (hh, i) is dim 128hh + 8c + i, built by v_perm
-//    from 16-byte pieces of 8 positions. Accumulator acc[ct][hh][i][ii] = O^T[dim 128hh + 32g4 +
-//    8ii + i][column c].
+//    4g4 + (e&3). The V^T A operands (which dims a lane holds) are the caller's choice; the
+//    softmax only rescales the NACC accumulators of each column tile.
 //  * Online softmax per column in the log2 domain with lazy rescaling: a column's reference max
 //    only moves when a score exceeds it by more than LAZY_TAU, so p = exp2(s - m_ref) <= 2^TAU
 //    and the accumulators are rescaled rarely. O/L is unchanged mathematically, and each column's
@@ -47,11 +46,11 @@ __device__ __forceinline__ void qk_tile(const u32x4_t* k_lds, const bf16x8_t (&q
 // Online softmax of one tile. MASK: positions >= Lcol[ct] are excluded (needed only on tiles that
 // reach past the shortest attended length among the real columns). SPLIT: P goes to the PV MFMA
 // as bf16 hi + lo terms (~2^-17 relative) instead of one bf16 term (2^-9).
-template <int NT, bool MASK, bool SPLIT>
+template <int NT, bool MASK, bool SPLIT, int NACC>
 __device__ __forceinline__ void softmax_tile(const f32x4_t (&sacc)[NT][2], int p0,
                                              const int (&Lcol)[NT], float scale_log2, int g4,
                                              float (&m)[NT], float (&l)[NT],
-                                             f32x4_t (&acc)[NT][2][8], u32x4_t (&pb_hi)[NT],
+                                             f32x4_t (&acc)[NT][NACC], u32x4_t (&pb_hi)[NT],
                                              u32x4_t (&pb_lo)[NT]) {
   float corr[NT];
   bool moved = false;
@@ -101,17 +100,16 @@ __device__ __forceinline__ void softmax_tile(const f32x4_t (&sacc)[NT][2], int p
 #pragma unroll
     for (int ct = 0; ct < NT; ++ct)
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[ct][hh][i] *= corr[ct];
+      for (int a = 0; a < NACC; ++a) acc[ct][a] *= corr[ct];
   }
 }
 
-// O^T += V^T P^T for dims [128hh, 128hh + 128): vr[e] = 16 bytes of V row P(g4, e), dims
-// 128hh + 8c + [0, 8).
+// O^T += V^T P^T for dims [128hh, 128hh + 128) (the prefill layout): vr[e] = 16 bytes of V row
+// P(g4, e), dims 128hh + 8c + [0, 8). M-tile i of the half has row c = dim 128hh + 8c + i, so
+// acc[ct][8hh + i][ii] = O^T[dim 128hh + 32g4 + 8ii + i][column c].
 template <int NT, bool SPLIT>
 __device__ __forceinline__ void pv_half(const u32x4_t (&vr)[8], int hh, const u32x4_t (&pb_hi)[NT],
-                                        const u32x4_t (&pb_lo)[NT], f32x4_t (&acc)[NT][2][8]) {
+                                        const u32x4_t (&pb_lo)[NT], f32x4_t (&acc)[NT][16]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     u32x4_t a;
@@ -119,9 +117,31 @@ __device__ __forceinline__ void pv_half(const u32x4_t (&vr)[8], int hh, const u3
     for (int d = 0; d < 4; ++d) a[d] = interleave_halves(vr[2 * d][i >> 1], vr[2 * d + 1][i >> 1], i & 1);
 #pragma unroll
     for (int ct = 0; ct < NT; ++ct) {
-      acc[ct][hh][i] = mfma16x16x32(as_bf16x8(a), as_bf16x8(pb_hi[ct]), acc[ct][hh][i]);
+      acc[ct][8 * hh + i] = mfma16x16x32(as_bf16x8(a), as_bf16x8(pb_hi[ct]), acc[ct][8 * hh + i]);
       if constexpr (SPLIT)
-        acc[ct][hh][i] = mfma16x16x32(as_bf16x8(a), as_bf16x8(pb_lo[ct]), acc[ct][hh][i]);
+        acc[ct][8 * hh + i] = mfma16x16x32(as_bf16x8(a), as_bf16x8(pb_lo[ct]), acc[ct][8 * hh + i]);
+    }
+  }
+}
+
+// O^T += V^T P^T for one 64-dim quarter of V (the decode layout): vr[e] = 8 bytes of V row
+// P(g4, e), quarter dims 4c + [0, 4). M-tile mt has row c = quarter dim 4c + mt, so
+// acc[ct][mt][i] = O^T[quarter dim 16g4 + 4i + mt][column c]: each lane ends up holding 16
+// consecutive dims (16g4 + [0, 16)) of its column.
+template <int NT, bool SPLIT>
+__device__ __forceinline__ void pv_quarter(const u32x2_t (&vr)[8], const u32x4_t (&pb_hi)[NT],
+                                           const u32x4_t (&pb_lo)[NT], f32x4_t (&acc)[NT][4]) {
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    u32x4_t a;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      a[d] = interleave_halves(vr[2 * d][mt >> 1], vr[2 * d + 1][mt >> 1], mt & 1);
+#pragma unroll
+    for (int ct = 0; ct < NT; ++ct) {
+      acc[ct][mt] = mfma16x16x32(as_bf16x8(a), as_bf16x8(pb_hi[ct]), acc[ct][mt]);
+      if constexpr (SPLIT)
+        acc[ct][mt] = mfma16x16x32(as_bf16x8(a), as_bf16x8(pb_lo[ct]), acc[ct][mt]);
     }
   }
 }

@@ -12,6 +12,7 @@ constexpr int WAVE = 64;     // CDNA wavefront
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------- bf16 rounding
 // torch rounds every bf16 op result to nearest-even; these model one such rounding.
@@ -45,15 +46,25 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// Max / sum across the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48).
-__device__ __forceinline__ float group4_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  return fmaxf(v, __shfl_xor(v, 32));
+// Max / sum across the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48) with the gfx950
+// VALU lane swaps instead of an LDS-crossbar permute. permlane16_swap(v, v) returns, per lane,
+// the values of 16-lane rows (0,0,2,2) and (1,1,3,3); permlane32_swap(v, v) returns the low and
+// the high 32 lanes. Combining the pair is the xor-16 (then xor-32) butterfly, and the lower
+// row's value is always the first operand, so every lane computes the same sum bit for bit.
+__device__ __forceinline__ float xor16_pair(float v, bool sum) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  const float a = __uint_as_float(p[0]), b = __uint_as_float(p[1]);
+  return sum ? a + b : fmaxf(a, b);
 }
-__device__ __forceinline__ float group4_sum(float v) {
-  v += __shfl_xor(v, 16);
-  return v + __shfl_xor(v, 32);
+__device__ __forceinline__ float xor32_pair(float v, bool sum) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  const float a = __uint_as_float(p[0]), b = __uint_as_float(p[1]);
+  return sum ? a + b : fmaxf(a, b);
 }
+__device__ __forceinline__ float group4_max(float v) { return xor32_pair(xor16_pair(v, false), false); }
+__device__ __forceinline__ float group4_sum(float v) { return xor32_pair(xor16_pair(v, true), true); }
 
 // ---------------------------------------------------------------------------- buffer loads
 // Raw buffer resource over [base, base + bytes). Loads whose dword lies past `bytes` return 0
@@ -90,6 +101,17 @@ template <int N>
 __device__ __forceinline__ void vmcnt_wait() {
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier for a ring of LDS-DMA stages: s_barrier between compiler-only fences (LDS
+// accesses are not moved across it) but without the hardware waits of __syncthreads(), whose
+// workgroup-scope release drains every outstanding LDS-DMA load. The caller has already waited
+// (vmcnt) for the DMA loads that the other waves must see; its own earlier LDS reads have
+// completed because their results were consumed.
+__device__ __forceinline__ void barrier_no_drain() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
