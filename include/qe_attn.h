@@ -44,7 +44,7 @@ hipError_t qe_attn_prep(const void* qg, const void* k, const void* v, long ldp, 
  * Two launches: split-KV partials over fixed slices of qe_attn_split_size(max_len, NS)
  * positions, then a log-sum-exp combine with the fused sigmoid gate. Row t of an n-row call is
  * bit-identical to a 1-row call at position pos+t. Valid: 1 <= n <= 8, Hq % Hkv == 0,
- * (Hq/Hkv)*n <= 64, NS >= 1, (max_len+128)*512 < 2^32, 16-byte aligned q/kc/vc/part_o.
+ * (Hq/Hkv)*n <= 64, NS >= 1, (max_len+32)*512 < 2^32, 16-byte aligned q/kc/vc/part_o.
  * Replaces launch_attn_decode (reference csrc/ops.h:28-30, csrc/attn.cu:165-172). */
 hipError_t qe_attn_decode(const void* q, const void* kc, const void* vc, const int* pos,
                           const void* qg, long ldp, float* part_o, float* part_ml, void* out,
