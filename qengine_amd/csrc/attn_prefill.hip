@@ -6,7 +6,9 @@
 //
 // Design (compute-bound, MFMA):
 //  * Workgroup = 128 consecutive query rows of one q head: 4 waves x 32 rows, each wave's rows are
-//    two 16-column MFMA tiles. Workgroups run heaviest (longest attended prefix) first.
+//    two 16-column MFMA tiles. Workgroups are dispatched heaviest (longest attended prefix) first
+//    over the whole grid, which balances the causal triangle across the CUs, and the workgroups of
+//    one KV head are placed on the same XCDs (one L2 per XCD).
 //  * K/V tiles of 32 positions are streamed into a 4-stage LDS ring by LDS DMA (each wave fetches
 //    8 rows, three tiles ahead, one barrier per tile) and shared by the 4 waves. K is
 //    XOR-swizzled for conflict-free operand reads.
@@ -38,6 +40,8 @@ constexpr int TILE_U4 = BN * ROW_CHUNKS;        // 16-byte slots per K (or V) ti
 constexpr int STAGE_U4 = 2 * TILE_U4;           // K tile then V tile (32 KB)
 constexpr int STAGES = 4;                       // LDS ring of tiles
 constexpr int AHEAD = STAGES - 1;               // tiles in flight beyond the one computed
+constexpr int PF_CPOL = 0;                      // cached loads: every row block re-reads its KV head
+constexpr int XCDS = 8;                         // MI355X: 8 XCDs, each with its own L2
 
 // Issue this wave's 8 LDS-DMA loads of tile [p0, p0 + 32): rows 8w .. 8w+7 of K (swizzled) and V.
 __device__ __forceinline__ void issue_tile(u32x4_t* stage, __amdgpu_buffer_rsrc_t krs,
@@ -46,14 +50,14 @@ __device__ __forceinline__ void issue_tile(u32x4_t* stage, __amdgpu_buffer_rsrc_
   for (int j = 0; j < 4; ++j) {
     const int r = 8 * w + 2 * j + (lane >> 5);
     const int q = (lane & 31) ^ (r & 15);
-    buffer_load16_to_lds(krs, (uint32_t)(p0 + r) * (HD * 2) + q * 16,
-                         stage + (8 * w + 2 * j) * ROW_CHUNKS);
+    buffer_load16_to_lds<PF_CPOL>(krs, (uint32_t)(p0 + r) * (HD * 2) + q * 16,
+                                  stage + (8 * w + 2 * j) * ROW_CHUNKS);
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r = 8 * w + 2 * j + (lane >> 5);
-    buffer_load16_to_lds(vrs, (uint32_t)(p0 + r) * (HD * 2) + (lane & 31) * 16,
-                         stage + TILE_U4 + (8 * w + 2 * j) * ROW_CHUNKS);
+    buffer_load16_to_lds<PF_CPOL>(vrs, (uint32_t)(p0 + r) * (HD * 2) + (lane & 31) * 16,
+                                  stage + TILE_U4 + (8 * w + 2 * j) * ROW_CHUNKS);
   }
 }
 
@@ -99,11 +103,24 @@ __global__ void __launch_bounds__(WAVES * WAVE)
 attn_prefill_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
                     const __bf16* __restrict__ vc, const int* __restrict__ pos_ptr,
                     const __bf16* __restrict__ qg, long ldp, __bf16* __restrict__ out, long ldo,
-                    int T, int Hq, int Hkv, int max_len, float scale_log2) {
-  const int nblk = gridDim.x;
-  const int blk = nblk - 1 - blockIdx.x;  // heaviest (latest) row block first
-  const int h = blockIdx.y;
-  const int g = h / (Hq / Hkv);
+                    int T, int Hq, int Hkv, int max_len, float scale_log2, int xcd_split) {
+  const int grp = Hq / Hkv;
+  const int nblk = (T + BQ - 1) / BQ;
+  int blk, h;
+  if (xcd_split > 0) {
+    // Workgroups are dispatched round-robin over the XCDs (linear id L -> XCD L % 8). The
+    // xcd_split XCDs 8g/Hkv .. serve KV head g only, taking turns along its work list (row block
+    // heaviest first, then q head), so the workgroups that read one KV head's cache share an L2
+    // and every XCD gets the same mix of heavy and light blocks.
+    const int L = blockIdx.x, x = L % XCDS;
+    const int i = (L / XCDS) * xcd_split + x % xcd_split;  // index in KV head g's work list
+    blk = nblk - 1 - i / grp;
+    h = (x / xcd_split) * grp + i % grp;
+  } else {
+    blk = nblk - 1 - (int)(blockIdx.x / Hq);  // heaviest (latest) row block first
+    h = blockIdx.x % Hq;
+  }
+  const int g = h / grp;
   const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
   const int c = lane & 15, g4 = lane >> 4;
   const int pos0 = pos_ptr[0];
@@ -205,16 +222,23 @@ extern "C" hipError_t qe_attn_prefill(const void* q, const void* kc, const void*
                                       long ldo, int T, int Hq, int Hkv, int max_len, float scale,
                                       hipStream_t stream) {
   auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  if (T < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || max_len < 1 || !pos || Hq > 65535)
+  if (T < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || max_len < 1 || !pos ||
+      (long)((T + prefill::BQ - 1) / prefill::BQ) * Hq > 0x7fffffffL)
     return hipErrorInvalidValue;
   if (!a16(q) || !a16(kc) || !a16(vc) || !a16(qg) || !a16(out) || ldp % 8 != 0 || ldo % 8 != 0)
     return hipErrorInvalidValue;
   if ((unsigned long long)(max_len + (prefill::AHEAD + 2) * prefill::BN) * HD * 2 >= (1ull << 32))
     return hipErrorInvalidValue;
   const int nblk = (T + prefill::BQ - 1) / prefill::BQ;
-  prefill::attn_prefill_kernel<<<dim3(nblk, Hq), dim3(prefill::WAVES * WAVE), 0, stream>>>(
+  // KV-head-per-XCD placement when the heads divide the XCDs evenly and every XCD of a head gets
+  // the same number of workgroups; otherwise plain heaviest-first order.
+  const int per_head = prefill::XCDS % Hkv == 0 ? prefill::XCDS / Hkv : 0;
+  const int xcd_split =
+      per_head > 0 && (nblk * (Hq / Hkv)) % per_head == 0 ? per_head : 0;
+  prefill::attn_prefill_kernel<<<dim3(nblk * Hq), dim3(prefill::WAVES * WAVE), 0, stream>>>(
       static_cast<const __bf16*>(q), static_cast<const __bf16*>(kc),
       static_cast<const __bf16*>(vc), pos, static_cast<const __bf16*>(qg), ldp,
-      static_cast<__bf16*>(out), ldo, T, Hq, Hkv, max_len, scale * 1.4426950408889634f);
+      static_cast<__bf16*>(out), ldo, T, Hq, Hkv, max_len, scale * 1.4426950408889634f,
+      xcd_split);
   return hipGetLastError();
 }

@@ -89,10 +89,13 @@ __device__ __forceinline__ u32x4_t buffer_load16_stream(__amdgpu_buffer_rsrc_t r
 // 16 bytes per lane from a buffer straight into LDS (gfx950 LDS DMA, non-temporal): lane i of the
 // wave writes lds_base + 16*i. lds_base must be wave-uniform. The compiler does not order later
 // LDS reads after this write: wait with vmcnt_wait() first.
+// CPOL selects the cache policy: CPOL_NT for data read once (decode's KV stream), 0 for data that
+// other workgroups read again soon (prefill's K/V tiles).
+template <int CPOL = CPOL_NT>
 __device__ __forceinline__ void buffer_load16_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t byte_off,
                                                      void* lds_base) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(
-      r, (__attribute__((address_space(3))) void*)lds_base, 16, (int)byte_off, 0, 0, CPOL_NT);
+      r, (__attribute__((address_space(3))) void*)lds_base, 16, (int)byte_off, 0, 0, CPOL);
 }
 
 // s_waitcnt vmcnt(N): at most N vector-memory loads of this wave still outstanding (gfx9
