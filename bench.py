@@ -216,7 +216,22 @@ def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
                      "hbm_frac": round(alg_bytes_layer(L) / (us * 1e3) / HBM_PEAK_GBS, 4)}
     del kcs, vcs
 
-    # cfg 5: chunked prefill, 2048 rows appended to a 2048-position cache
+    res.update(bench_prefill(torch, C, steps, warmup))
+    return res
+
+
+def bench_prefill(torch, C, steps: int, warmup: int) -> dict:
+    """a 2048-row causal chunk appended to a 2048-position cache (attn_prep_chunk
+    + attn_prefill), timed as graph replays. FLOPs = 4 * D * Hq * sum of attended lengths."""
+    dev, BF = "cuda", torch.bfloat16
+    gen = torch.Generator(device=dev).manual_seed(5)
+    res = {}
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, device=dev, generator=gen) * scale).to(BF)
+
+    inv = (1.0 / (1e7 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 64))).to(dev)
+    qnw, knw = rnd(D, scale=0.3), rnd(D, scale=0.3)
     T, pos0 = 2048, 2048
     L = pos0 + T
     kc, vc = rnd(HKV, L, D), rnd(HKV, L, D)
@@ -290,6 +305,8 @@ def main():
     ap.add_argument("--lengths", default="4096,16384,32768")
     ap.add_argument("--ns", type=int, default=0, help="split count (0 = default policy)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only BASELINE config 5 (chunked prefill); prints its timing as JSON")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other BASELINE configs (1, 3, 4, 5)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -317,6 +334,9 @@ def main():
     import qengine_amd as qa
     C = qa._C
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.prefill_only:
+        print(json.dumps(bench_prefill(torch, C, args.steps, args.warmup)))
+        return
     lengths = [int(x) for x in args.lengths.split(",") if x]
     if HEADLINE_L not in lengths:
         lengths.append(HEADLINE_L)

@@ -5,16 +5,16 @@
 // through its n <= 8 row decode path (engine.py:542-573).
 //
 // Design (compute-bound, MFMA):
-//  * Workgroup = 128 consecutive query rows of one q head: 4 waves x 32 rows, each wave's rows are
-//    two 16-column MFMA tiles. Workgroups are dispatched heaviest (longest attended prefix) first
+//  * Workgroup = 128 consecutive query rows of one q head: 8 waves x 16 rows (one 16-column MFMA
+//    tile per wave, two waves per SIMD). Workgroups are dispatched heaviest (longest attended prefix) first
 //    over the whole grid, which balances the causal triangle across the CUs, and the workgroups of
 //    one KV head are placed on the same XCDs (one L2 per XCD).
 //  * K/V tiles of 32 positions are streamed into a 4-stage LDS ring by LDS DMA (each wave fetches
-//    8 rows, three tiles ahead, one barrier per tile) and shared by the 4 waves. K is
-//    XOR-swizzled for conflict-free operand reads.
-//  * Per tile and wave: S^T = K Q^T (32 MFMA 16x16x32), online softmax per column in the log2
-//    domain with lazy rescaling, O^T += V^T P^T (32 MFMA). Waves whose rows attend fewer than
-//    512 positions pass P as bf16 hi + lo terms (64 MFMA) for fp32-class accuracy; longer rows
+//    4 rows of K and of V, three tiles ahead, one barrier per tile) and shared by the 8 waves. K
+//    is XOR-swizzled for conflict-free operand reads (rocprofv3: zero LDS bank conflicts).
+//  * Per tile and wave: S^T = K Q^T (16 MFMA 16x16x32), online softmax per column in the log2
+//    domain with lazy rescaling, O^T += V^T P^T (16 MFMA). Waves whose rows attend fewer than
+//    512 positions pass P as bf16 hi + lo terms (32 MFMA) for fp32-class accuracy; longer rows
 //    average the bf16 rounding of P away. Q lives in registers as the B operand, O^T in
 //    accumulation registers. The tile math is shared with decode (attn_tile.hpp).
 //  * The tile loop body is branch-free: unmasked tiles (below the wave's shortest row) and masked
@@ -27,8 +27,11 @@
 namespace qe {
 namespace prefill {
 
-constexpr int WAVES = 4;
-constexpr int ROWS_PER_WAVE = 32;               // two 16-column MFMA tiles
+// Two waves per SIMD: one wave's softmax (VALU) overlaps the other's MFMAs. With 16 rows per
+// wave the tile loop fits 218 VGPRs. (Measured on MI355X at config 5: 4 waves x 32 rows, one wave
+// per SIMD, ran 328 us; 8 waves x 16 rows runs 271 us.)
+constexpr int WAVES = 8;
+constexpr int ROWS_PER_WAVE = 16;               // one 16-column MFMA tile per wave
 constexpr int NT = ROWS_PER_WAVE / 16;
 constexpr int BQ = WAVES * ROWS_PER_WAVE;       // 128 query rows per workgroup
 using tile::BN;                                 // cache positions per step
@@ -40,24 +43,29 @@ constexpr int TILE_U4 = BN * ROW_CHUNKS;        // 16-byte slots per K (or V) ti
 constexpr int STAGE_U4 = 2 * TILE_U4;           // K tile then V tile (32 KB)
 constexpr int STAGES = 4;                       // LDS ring of tiles
 constexpr int AHEAD = STAGES - 1;               // tiles in flight beyond the one computed
+constexpr int LOAD_ROWS = BN / WAVES;            // K and V rows each wave fetches per tile
+constexpr int LOAD_INSTR = LOAD_ROWS / 2;        // two 512-byte rows per LDS-DMA instruction
+constexpr int LOADS_PER_TILE = 2 * LOAD_INSTR;   // K then V
+static_assert(LOAD_ROWS % 2 == 0 && LOADS_PER_TILE * AHEAD < 64, "tile split over the waves");
 constexpr int PF_CPOL = 0;                      // cached loads: every row block re-reads its KV head
 constexpr int XCDS = 8;                         // MI355X: 8 XCDs, each with its own L2
 
-// Issue this wave's 8 LDS-DMA loads of tile [p0, p0 + 32): rows 8w .. 8w+7 of K (swizzled) and V.
+// Issue this wave's LDS-DMA loads of tile [p0, p0 + 32): rows LOAD_ROWS*w .. +LOAD_ROWS of K
+// (swizzled) and of V.
 __device__ __forceinline__ void issue_tile(u32x4_t* stage, __amdgpu_buffer_rsrc_t krs,
                                            __amdgpu_buffer_rsrc_t vrs, int p0, int w, int lane) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = 8 * w + 2 * j + (lane >> 5);
+  for (int j = 0; j < LOAD_INSTR; ++j) {
+    const int r = LOAD_ROWS * w + 2 * j + (lane >> 5);
     const int q = (lane & 31) ^ (r & 15);
     buffer_load16_to_lds<PF_CPOL>(krs, (uint32_t)(p0 + r) * (HD * 2) + q * 16,
-                                  stage + (8 * w + 2 * j) * ROW_CHUNKS);
+                                  stage + (LOAD_ROWS * w + 2 * j) * ROW_CHUNKS);
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = 8 * w + 2 * j + (lane >> 5);
+  for (int j = 0; j < LOAD_INSTR; ++j) {
+    const int r = LOAD_ROWS * w + 2 * j + (lane >> 5);
     buffer_load16_to_lds<PF_CPOL>(vrs, (uint32_t)(p0 + r) * (HD * 2) + (lane & 31) * 16,
-                                  stage + TILE_U4 + (8 * w + 2 * j) * ROW_CHUNKS);
+                                  stage + TILE_U4 + (LOAD_ROWS * w + 2 * j) * ROW_CHUNKS);
   }
 }
 
@@ -78,7 +86,7 @@ __device__ __forceinline__ void run_tiles(int j0, int j1, int Lwave, u32x4_t* ld
     const u32x4_t* kt = lds + (j % STAGES) * STAGE_U4;
     const u32x4_t* vt = kt + TILE_U4;
     const int p0 = j * BN;
-    vmcnt_wait<8 * (AHEAD - 1)>();  // this wave's loads of tile j are done
+    vmcnt_wait<LOADS_PER_TILE * (AHEAD - 1)>();  // this wave's loads of tile j are done
     __syncthreads();                // ... and every wave's; tile j-1's stage is free
     issue_tile(lds + ((j + AHEAD) % STAGES) * STAGE_U4, krs, vrs, p0 + AHEAD * BN, w, lane);
     if (p0 >= Lwave) continue;      // tiles past this wave's rows contribute nothing
