@@ -108,8 +108,8 @@ template <int WAVES>
 constexpr int lds_k_bytes() { return WAVES * TILE * HD * 2; }  // 16 KB per wave
 
 // part_o [n][Hq][NS][HD] (unnormalised O), part_ml [n][Hq][NS][2] = (max in log2 units, sum).
-// NT = 1 (decode, 1-2 rows) fits in 256 registers, which lets two workgroups share a CU (one
-// streams while the other computes); the multi-row verify shapes need the whole register file.
+// NT = 1 (decode, 1-2 rows at GQA 6) fits in 256 registers, which lets two workgroups share a CU;
+// NT = 2 (3-5 rows) needs the whole register file. Wider shapes use attn_partials_cols_kernel.
 template <int NT, int WAVES = waves_for<NT>()>
 __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, 2)))
 attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
@@ -246,6 +246,187 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc
   }
 }
 
+// Multi-row variant (NT >= 3 column tiles: six or more rows at GQA 6, up to 64 columns).
+// A workgroup (slice, KV head) holds 4 position subsets x NT/CPW waves: wave (sub, rank) owns
+// column tiles [rank*CPW, +CPW) for the slice's tiles k = sub (mod 4), the same tiles that wave
+// `sub` of attn_partials_kernel processes, with the same per-column arithmetic, and the 4 subsets
+// merge in the same order 0..3. So every column's partial is bit-identical to what the one-tile
+// kernel computes for it, which keeps row t of an n-row call equal to a 1-row call. The waves of a
+// subset share its K and V tile through LDS (LDS DMA, as in prefill); each wave keeps only its own
+// columns' state in registers (<= 170 VGPRs at three waves per SIMD), where the one-tile kernel
+// would need all NT column tiles per wave and spill.
+namespace cols {
+constexpr int SUBSETS = 4;
+constexpr int TILE_U4 = TILE * ROW_CHUNKS;   // 16-byte slots of one K (or V) tile: 16 KB
+constexpr int REGION_U4 = 2 * TILE_U4;       // a subset's K tile then V tile
+}  // namespace cols
+
+template <int NT, int CPW>
+__global__ void __launch_bounds__(cols::SUBSETS * (NT / CPW) * WAVE)
+attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
+                          const __bf16* __restrict__ vc, const int* __restrict__ pos_ptr,
+                          float* __restrict__ part_o, float* __restrict__ part_ml, int n, int Hq,
+                          int Hkv, int max_len, int NS, int CH, float scale_log2) {
+  static_assert(NT % CPW == 0, "column tiles split evenly over the waves of a subset");
+  constexpr int SUB = cols::SUBSETS;
+  constexpr int WPS = NT / CPW;  // waves per subset
+  const int s = blockIdx.x, g = blockIdx.y;
+  const int grp = Hq / Hkv;
+  const int pos0 = pos_ptr[0];
+  const int Lmax = min(pos0 + n, max_len);
+  const int beg = s * CH;
+  if (beg >= Lmax) return;  // uniform per workgroup
+  const int end = min(beg + CH, Lmax);
+
+  const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+  const int sub = w % SUB, rank = w / SUB;
+  const int c = lane & 15, g4 = lane >> 4;
+  const int ncols = grp * n;
+
+  __shared__ __attribute__((aligned(16))) u32x4_t lds[SUB * cols::REGION_U4];  // 128 KB
+  __shared__ float s_m[SUB][16 * NT], s_l[SUB][16 * NT];
+
+  bf16x8_t qb[CPW][8];
+  int Lcol[CPW];
+#pragma unroll
+  for (int u = 0; u < CPW; ++u) {
+    const int col = (rank * CPW + u) * 16 + c;
+    if (col < ncols) {
+      const int t = col / grp, j = col - t * grp;
+      Lcol[u] = min(pos0 + t + 1, max_len);
+      const u32x4_t* src =
+          reinterpret_cast<const u32x4_t*>(q + (size_t)t * Hq * HD + (size_t)(g * grp + j) * HD);
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) qb[u][ks] = as_bf16x8(src[4 * ks + g4]);
+    } else {
+      Lcol[u] = 0;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) qb[u][ks] = as_bf16x8(u32x4_t{0u, 0u, 0u, 0u});
+    }
+  }
+
+  const int Lmin = min(pos0 + 1, max_len);
+  const size_t head_off = (size_t)g * max_len * HD;
+  const uint32_t bytes = (uint32_t)end * (uint32_t)(HD * 2);
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kc + head_off, bytes);
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vc + head_off, bytes);
+
+  float m[CPW], l[CPW];
+  f32x4_t acc[CPW][16];
+#pragma unroll
+  for (int u = 0; u < CPW; ++u) {
+    m[u] = -INFINITY;
+    l[u] = 0.f;
+#pragma unroll
+    for (int a = 0; a < 16; ++a) acc[u][a] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  u32x4_t* kt = lds + sub * cols::REGION_U4;
+  const u32x4_t* vt = kt + cols::TILE_U4;
+  const int ntiles = (end - beg + TILE - 1) / TILE;
+  const int rounds = (ntiles + SUB - 1) / SUB;
+  for (int r = 0; r < rounds; ++r) {
+    const int p0 = beg + (r * SUB + sub) * TILE;  // this subset's tile in round r
+    const bool has = p0 < end;                     // uniform per subset
+    if (has) {
+      // The subset's WPS waves share its 32 LDS-DMA loads: 16 of K (rows 2i, 2i+1, swizzled as
+      // k_slot) and 16 of V (row-major), one KB of contiguous cache each.
+      for (int i = rank; i < 32; i += WPS) {
+        const int j = i & 15, row = 2 * j + (lane >> 5);
+        if (i < 16)
+          buffer_load16_to_lds(krs, (uint32_t)(p0 + row) * (HD * 2) + ((lane & 31) ^ (row & 15)) * 16,
+                               kt + 2 * j * ROW_CHUNKS);
+        else
+          buffer_load16_to_lds(vrs, (uint32_t)(p0 + row) * (HD * 2) + (lane & 31) * 16,
+                               kt + cols::TILE_U4 + 2 * j * ROW_CHUNKS);
+      }
+    }
+    vmcnt_wait<0>();
+    __syncthreads();  // every wave's loads of this round have landed
+    if (has) {
+      f32x4_t sacc[CPW][2];
+      tile::qk_tile<CPW>(kt, qb, c, g4, sacc);
+      u32x4_t pb_hi[CPW], pb_lo[CPW];
+      if (p0 + TILE > Lmin)
+        tile::softmax_tile<CPW, true, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
+      else
+        tile::softmax_tile<CPW, false, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        u32x4_t vr[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          vr[e] = vt[(16 * (e >> 2) + 4 * g4 + (e & 3)) * ROW_CHUNKS + 16 * hh + c];
+        tile::pv_half<CPW, true>(vr, hh, pb_hi, pb_lo, acc);
+      }
+    }
+    __syncthreads();  // this round's tiles are read before the next round overwrites them
+  }
+
+  // ---- merge the 4 subsets in order 0..3 (as attn_partials_kernel merges its waves)
+#pragma unroll
+  for (int u = 0; u < CPW; ++u) {
+    l[u] = group4_sum(l[u]);
+    if (g4 == 0) {
+      s_m[sub][(rank * CPW + u) * 16 + c] = m[u];
+      s_l[sub][(rank * CPW + u) * 16 + c] = l[u];
+    }
+  }
+  __syncthreads();
+  float wsc[CPW][SUB];
+#pragma unroll
+  for (int u = 0; u < CPW; ++u) {
+    const int col = (rank * CPW + u) * 16 + c;
+    float M = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < SUB; ++v) M = fmaxf(M, s_m[v][col]);
+    float L = 0.f;
+#pragma unroll
+    for (int v = 0; v < SUB; ++v) {
+      const float mv = s_m[v][col];
+      wsc[u][v] = mv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv - M);
+      L += s_l[v][col] * wsc[u][v];
+    }
+    if (sub == 0 && g4 == 0 && col < ncols) {
+      const int t = col / grp, head = g * grp + (col - t * grp);
+      float* ml = part_ml + (((size_t)t * Hq + head) * NS + s) * 2;
+      ml[0] = M;
+      ml[1] = L;
+    }
+  }
+  f32x4_t (*s_acc)[16][WAVE] = reinterpret_cast<f32x4_t (*)[16][WAVE]>(lds);
+  static_assert(SUB * 16 * WAVE * 16 <= SUB * cols::REGION_U4 * 16, "merge buffer fits the ring");
+  for (int rr = 0; rr < WPS; ++rr) {
+#pragma unroll
+    for (int u = 0; u < CPW; ++u) {
+      const int col = (rr * CPW + u) * 16 + c;
+      if (rank == rr && col < ncols) {
+#pragma unroll
+        for (int a = 0; a < 16; ++a) s_acc[sub][a][lane] = acc[u][a];
+      }
+      __syncthreads();
+      if (rank == rr && col < ncols) {
+        const int h = sub >> 1, i0 = 4 * (sub & 1);
+        f32x4_t mo[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          f32x4_t sum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int v = 0; v < SUB; ++v) sum += s_acc[v][8 * h + i0 + k][lane] * wsc[u][v];
+          mo[k] = sum;
+        }
+        const int t = col / grp, head = g * grp + (col - t * grp);
+        float* dst = part_o + (((size_t)t * Hq + head) * NS + s) * HD + 128 * h + 32 * g4 + i0;
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii)
+          reinterpret_cast<f32x4_t*>(dst + 8 * ii)[0] =
+              f32x4_t{mo[0][ii], mo[1][ii], mo[2][ii], mo[3][ii]};
+      }
+      __syncthreads();
+    }
+  }
+}
+
 // Log-sum-exp merge of the slices holding row t's positions + fused sigmoid output gate.
 // One wave per (head h, row t, 64-dim chunk z). Lane group sg = lane/16 owns slices
 // s = sg (mod 4) and 4 dims per lane. The loads of a batch of COMBINE_BATCH slices are all
@@ -351,11 +532,13 @@ static hipError_t launch_partials(const void* q, const void* kc, const void* vc,
   const auto* Q = static_cast<const __bf16*>(q);
   const auto* K = static_cast<const __bf16*>(kc);
   const auto* V = static_cast<const __bf16*>(vc);
+  // NT = 1, 2: every wave holds all column tiles (measured fastest at 1-5 rows, GQA 6).
+  // NT = 3, 4: one subset wave per column tile (the one-tile kernel would spill: 2.3-2.8x slower).
   switch (NT) {
     case 1: attn_partials_kernel<1><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
     case 2: attn_partials_kernel<2><<<grid, dim3(waves_for<2>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
-    case 3: attn_partials_kernel<3><<<grid, dim3(waves_for<3>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
-    default: attn_partials_kernel<4><<<grid, dim3(waves_for<4>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
+    case 3: attn_partials_cols_kernel<3, 1><<<grid, dim3(cols::SUBSETS * 3 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
+    default: attn_partials_cols_kernel<4, 2><<<grid, dim3(cols::SUBSETS * 2 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
   }
   return hipGetLastError();
 }
