@@ -173,6 +173,35 @@ def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
     us = time_fn_graph(torch, cfg1, steps, warmup) * 1e3 / nl
     res["cfg1_prep_decode_1k"] = {"us_per_layer": round(us, 3),
                                   "GBps": round((alg_bytes_layer(L) + 45056) / (us * 1e3), 1)}
+
+    def cfg1_fused():
+        for kk, vv in zip(kcs, vcs):
+            C.attn_prep_decode(qg, k, v, qnw, knw, inv, pos, q, kk, vv, 1e-6, po, pml, out)
+    us = time_fn_graph(torch, cfg1_fused, steps, warmup) * 1e3 / nl
+    res["cfg1_prep_decode_1k_fused"] = {"us_per_layer": round(us, 3),
+                                        "GBps": round((alg_bytes_layer(L) + 45056) / (us * 1e3), 1)}
+    del kcs, vcs
+
+    # prep + decode per layer at KV 16384 (16 layers on distinct caches), separate and fused ops
+    L, nl = 16384, 16
+    kcs = [rnd(HKV, L, D) for _ in range(nl)]
+    vcs = [rnd(HKV, L, D) for _ in range(nl)]
+    ns16 = qa.default_splits(L, HKV)
+    po16, pml16 = qa.alloc_partials(1, HQ, ns16, dev)
+    pos16 = torch.tensor([L - 1], dtype=torch.int32, device=dev)
+
+    def sep16():
+        for kk, vv in zip(kcs, vcs):
+            C.attn_prep(qg, k, v, qnw, knw, inv, pos16, q, kk, vv, 1e-6)
+            C.attn_decode(q, kk, vv, pos16, qg, po16, pml16, out)
+
+    def fused16():
+        for kk, vv in zip(kcs, vcs):
+            C.attn_prep_decode(qg, k, v, qnw, knw, inv, pos16, q, kk, vv, 1e-6, po16, pml16, out)
+    for name, fn in (("prep_decode_16k", sep16), ("prep_decode_16k_fused", fused16)):
+        us = time_fn_graph(torch, fn, steps, warmup) * 1e3 / nl
+        res[name] = {"us_per_layer": round(us, 3),
+                     "GBps": round((alg_bytes_layer(L) + 45056) / (us * 1e3), 1)}
     del kcs, vcs
 
     # cfg 3: MTP verify, 5 rows at pos 4096 over 4096 cached + 5 new positions

@@ -51,6 +51,20 @@ hipError_t qe_attn_decode(const void* q, const void* kc, const void* vc, const i
                           long ldo, int n, int Hq, int Hkv, int max_len, int NS, float scale,
                           hipStream_t stream);
 
+/* qe_attn_prep followed by qe_attn_decode (same arguments; q_out is also the decode's q), in two
+ * launches instead of three: the split-KV kernel computes its q rows and writes the new K/V
+ * cache rows itself, then the combine runs. Every output (q_out, the written cache rows, out) is
+ * bit-identical to the two calls in sequence. Valid: the union of both ops' ranges (1 <= n <= 8,
+ * (Hq/Hkv)*n <= 64, ...); shapes wider than 32 columns ((Hq/Hkv)*n > 32) run the two ops.
+ * No counterpart in the reference, which overlaps the two launches with programmatic dependent
+ * launch instead (csrc/attn.cu:155, csrc/common.cuh:12-46; callers python/qengine/engine.py:455-458). */
+hipError_t qe_attn_prep_decode(const void* qg, const void* k, const void* v, long ldp,
+                               const void* qnw, const void* knw, const float* inv_freq,
+                               const int* pos, void* q_out, void* kc, void* vc, float* part_o,
+                               float* part_ml, void* out, long ldo, int n, int Hq, int Hkv,
+                               int max_len, int rd, int NS, float scale, float eps,
+                               hipStream_t stream);
+
 /* First half of qe_attn_decode: the split-KV partials only (part_o/part_ml filled for the slices
  * that hold positions). The pair is exported separately so that a sequence-sharded caller can
  * exchange partials between devices before combining, and so the partials kernel can be timed

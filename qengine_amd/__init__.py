@@ -27,6 +27,7 @@ from ._C import (  # noqa: E402,F401
     attn_prefill,
     attn_prep,
     attn_prep_chunk,
+    attn_prep_decode,
     set_pdl_launch,
     set_pdl_trigger,
     split_size,

@@ -25,6 +25,8 @@ SIGNATURES = {
     "qe_attn_decode_partials": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P]),
     "qe_attn_decode_combine": (_I, [_P, _P, _P, _P, _L, _P, _L, _I, _I, _I, _I, _P]),
     "qe_attn_prefill": (_I, [_P, _P, _P, _P, _P, _L, _P, _L, _I, _I, _I, _I, _F, _P]),
+    "qe_attn_prep_decode": (_I, [_P, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _I, _I,
+                                 _I, _I, _I, _I, _F, _F, _P]),
     "qe_attn_split_size": (_I, [_I, _I]),
     "qe_attn_version": (ctypes.c_char_p, []),
     "qe_set_pdl_trigger": (None, [_I]),
@@ -76,6 +78,14 @@ def decode(q, kc, vc, pos, qg, ldp, part_o, part_ml, out, ldo, n, hq, hkv, max_l
     return load().qe_attn_decode(_ptr(q), _ptr(kc), _ptr(vc), _ptr(pos), _ptr(qg), ldp,
                                  _ptr(part_o), _ptr(part_ml), _ptr(out), ldo, n, hq, hkv, max_len,
                                  ns, scale, _stream(stream))
+
+
+def prep_decode(qg, k, v, ldp, qnw, knw, inv_freq, pos, q_out, kc, vc, part_o, part_ml, out, ldo,
+                n, hq, hkv, max_len, rd, ns, scale=1.0 / 16, eps=1e-6, stream=None) -> int:
+    return load().qe_attn_prep_decode(_ptr(qg), _ptr(k), _ptr(v), ldp, _ptr(qnw), _ptr(knw),
+                                      _ptr(inv_freq), _ptr(pos), _ptr(q_out), _ptr(kc), _ptr(vc),
+                                      _ptr(part_o), _ptr(part_ml), _ptr(out), ldo, n, hq, hkv,
+                                      max_len, rd, ns, scale, eps, _stream(stream))
 
 
 def decode_partials(q, kc, vc, pos, part_o, part_ml, n, hq, hkv, max_len, ns, scale=1.0 / 16,

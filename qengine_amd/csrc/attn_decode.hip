@@ -23,6 +23,8 @@
 //    moved (an exact no-op).
 //  * Buffer resources bound the K/V reads to the slice: positions past it load as 0.
 //  * A second launch merges the slices (log-sum-exp) and applies the sigmoid gate.
+#include <utility>
+
 #include "attn_tile.hpp"
 #include "qe_attn.h"
 
@@ -107,22 +109,210 @@ __device__ __forceinline__ void wait_and_compute(const VTile& b, const u32x4_t* 
 template <int WAVES>
 constexpr int lds_k_bytes() { return WAVES * TILE * HD * 2; }  // 16 KB per wave
 
+// Inputs of the prep fused into the partials kernel (qe_attn_prep_decode); unused otherwise.
+struct PrepIn {
+  const __bf16* qg;   // rows [n][ldp]: per q head [q (256) | gate (256)]
+  const __bf16* k;    // rows [n][ldp]: Hkv*256
+  const __bf16* v;
+  long ldp;
+  const __bf16* qnw;
+  const __bf16* knw;
+  const float* inv_freq;
+  __bf16* q_out;      // [n][Hq*256]
+  int rd;
+  float eps;
+};
+
+// LDS of the fused prep: the group's q rows (bf16, 16-byte chunks, rows padded by one chunk so the
+// 16 columns a lane group reads hit different banks), per wave: the staged input rows of its items,
+// the two norm weight rows and inv_freq, one 256-float row for the rotate-half exchange; and the
+// rotary cos/sin table of the call's rows.
+constexpr int FQ_ROW_U4 = ROW_CHUNKS + 1;
+constexpr int PREP_WAVES = 4;
+constexpr int ROPE_TAB = 256;  // n * rd/2 entries, one per thread (the fused path's limit)
+template <int NT>
+struct PrepShape {
+  static constexpr int MAXI = (16 * NT + 8 + PREP_WAVES - 1) / PREP_WAVES;  // items per wave
+  static constexpr int PAIRS = (MAXI + 1) / 2;  // 16-byte loads of two rows per lane
+};
+template <int NT>
+struct FusedLds {
+  u32x4_t q[16 * NT][FQ_ROW_U4];
+  u32x4_t stage_x[PREP_WAVES][2 * PrepShape<NT>::PAIRS][ROW_CHUNKS];
+  u32x4_t stage_w[PREP_WAVES][2][ROW_CHUNKS];  // qnw, knw
+  float stage_f[PREP_WAVES][HD / 2];          // inv_freq (half <= 128)
+  float xn[PREP_WAVES][HD];
+  float cs[ROPE_TAB], sn[ROPE_TAB];
+};
+__shared__ __attribute__((aligned(16))) char fused_lds_raw[sizeof(FusedLds<2>)];
+template <int NT>
+__device__ __forceinline__ FusedLds<NT>& fused_lds() {
+  return *reinterpret_cast<FusedLds<NT>*>(fused_lds_raw);
+}
+__device__ __forceinline__ u32x4_t fused_q_lds(int col, int chunk) {
+  return reinterpret_cast<const u32x4_t*>(fused_lds_raw)[col * FQ_ROW_U4 + chunk];
+}
+
+// The prep of qe_attn_prep for this workgroup, one row ("item") per wave at a time and no
+// workgroup barrier inside an item: items are the ncols q rows of KV head g's group (to LDS, and
+// to q_out from slice 0) and the cache rows pos+t, t in [t_lo, t_hi), that lie in this slice;
+// item i goes to wave i % 4. Lane l holds dims l + 64r (r = 0..3), the prep kernel's thread
+// c = 64r + l, so the four wave butterflies and ((s0 + s1) + s2) + s3 are that kernel's reduction
+// tree, and every output is bit-identical to it.
+// The input rows are loaded with 16-byte loads (lanes 0-31 one row, 32-63 the next), a few per
+// wave, all before the caller's tile prefetch (loads return in order: a later load would wait for
+// the tile, and a wave can have only 63 loads outstanding), and staged through LDS into that layout.
+// The V rows are loaded at the end, only by the workgroup that writes cache rows.
+template <int NT>
+struct PrepRegs {
+  u32x4_t x[PrepShape<NT>::PAIRS], w, f;
+};
+
+template <int NT>
+__device__ __forceinline__ void fused_prep_load(PrepRegs<NT>& r, const PrepIn& pin, int g,
+                                                int grp, int n, int ncols, int t_lo, int t_hi) {
+  const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+  const int nitems = ncols + (t_hi - t_lo);
+  const int hl = lane >> 5, ch = lane & 31;  // row of the pair, 16-byte chunk of the row
+#pragma unroll
+  for (int P = 0; P < PrepShape<NT>::PAIRS; ++P) {
+    int it = (2 * P + hl) * PREP_WAVES + w;
+    it = it < nitems ? it : 0;  // slots past the end load row 0's q (discarded)
+    const bool isq = it < ncols;
+    const int t = isq ? it / grp : t_lo + (it - ncols);
+    const __bf16* src = isq ? pin.qg + (size_t)t * pin.ldp + (size_t)(g * grp + it % grp) * 2 * HD
+                            : pin.k + (size_t)t * pin.ldp + (size_t)g * HD;
+    r.x[P] = reinterpret_cast<const u32x4_t*>(src)[ch];
+  }
+  r.w = reinterpret_cast<const u32x4_t*>(hl ? pin.knw : pin.qnw)[ch];
+  const int half = pin.rd >> 1;  // a multiple of 4 on this path
+  r.f = reinterpret_cast<const u32x4_t*>(pin.inv_freq)[lane < half / 4 ? lane : 0];
+}
+
+template <int NT, int K>
+__device__ __forceinline__ void fused_prep_item(const PrepIn& pin, int s, int g, int grp, int Hq,
+                                                int ncols, int nitems, int pos0, int t_lo,
+                                                int max_len, __bf16* kc, __bf16* vc) {
+  FusedLds<NT>& L = fused_lds<NT>();
+  const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+  const int it = K * PREP_WAVES + w;
+  if (it >= nitems) return;  // uniform per wave
+  const int rd = pin.rd, half = rd >> 1;
+  float* xn = L.xn[w];
+  const __bf16* xrow = reinterpret_cast<const __bf16*>(&L.stage_x[w][K][0]);
+  const __bf16* wrow = reinterpret_cast<const __bf16*>(&L.stage_w[w][0][0]);
+  const bool isq = it < ncols;
+  const int t = isq ? it / grp : t_lo + (it - ncols);
+  float x[4], sr[4];
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    x[rr] = bf16_to_f32(xrow[lane + 64 * rr]);
+    sr[rr] = wave_sum_fast(x[rr] * x[rr]);
+  }
+  const float total = ((sr[0] + sr[1]) + sr[2]) + sr[3];
+  const float inv = 1.0f / sqrtf(total / (float)HD + pin.eps);
+  float xv[4];
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const float wgt = bf16_to_f32(wrow[(isq ? 0 : HD) + lane + 64 * rr]);
+    xv[rr] = round_bf16((x[rr] * inv) * (1.0f + wgt));
+    xn[lane + 64 * rr] = xv[rr];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float y[4];
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const int d = lane + 64 * rr;
+    y[rr] = xv[rr];
+    if (d < rd) {
+      const int e = t * half + (d < half ? d : d - half);
+      const float rot = d < half ? -xn[d + half] : xn[d - half];  // rotate_half
+      y[rr] = round_bf16(round_bf16(xv[rr] * L.cs[e]) + round_bf16(rot * L.sn[e]));
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // xn reads done before the next item
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (isq) {
+    const int head = g * grp + it % grp;
+    __bf16* qrow = reinterpret_cast<__bf16*>(&L.q[0][0]) + it * FQ_ROW_U4 * 8;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const __bf16 yb = f32_to_bf16(y[rr]);
+      qrow[lane + 64 * rr] = yb;
+      if (s == 0) pin.q_out[(size_t)t * Hq * HD + (size_t)head * HD + lane + 64 * rr] = yb;
+    }
+  } else {
+    const size_t dst = ((size_t)g * max_len + (pos0 + t)) * HD;
+    const __bf16* vrow = pin.v + (size_t)t * pin.ldp + (size_t)g * HD;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      kc[dst + lane + 64 * rr] = f32_to_bf16(y[rr]);
+      vc[dst + lane + 64 * rr] = vrow[lane + 64 * rr];  // bit for bit
+    }
+  }
+}
+
+// Ends with a workgroup barrier after which the q rows are readable in LDS and, in the workgroup
+// that writes cache rows, those writes have completed (so the waves' later tile loads see them).
+template <int NT, int... Ks>
+__device__ __forceinline__ void fused_prep_compute(const PrepRegs<NT>& r, const PrepIn& pin, int s,
+                                                   int g, int grp, int n, int Hq, int ncols,
+                                                   int pos0, int t_lo, int t_hi, int max_len,
+                                                   __bf16* kc, __bf16* vc,
+                                                   std::integer_sequence<int, Ks...>) {
+  FusedLds<NT>& L = fused_lds<NT>();
+  const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+  const int hl = lane >> 5, ch = lane & 31, half = pin.rd >> 1;
+#pragma unroll
+  for (int P = 0; P < PrepShape<NT>::PAIRS; ++P) L.stage_x[w][2 * P + hl][ch] = r.x[P];
+  L.stage_w[w][hl][ch] = r.w;
+  if (lane < half / 4) reinterpret_cast<u32x4_t*>(L.stage_f[w])[lane] = r.f;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int e = threadIdx.x;  // rotary table entry (row e / half, frequency e % half)
+  if (e < n * half) {
+    const RopeCS cs = rope_cs_f(pos0 + e / half, L.stage_f[w][e % half], pin.rd, 0);
+    L.cs[e] = cs.cs;
+    L.sn[e] = cs.sn;
+  }
+  lds_barrier();
+  const int nitems = ncols + (t_hi - t_lo);
+  (fused_prep_item<NT, Ks>(pin, s, g, grp, Hq, ncols, nitems, pos0, t_lo, max_len, kc, vc), ...);
+  if (t_hi > t_lo)
+    __syncthreads();  // release: the cache rows are written before any wave loads them
+  else
+    lds_barrier();    // only the q rows in LDS are shared; tile loads stay in flight
+}
+
 // part_o [n][Hq][NS][HD] (unnormalised O), part_ml [n][Hq][NS][2] = (max in log2 units, sum).
 // NT = 1 (decode, 1-2 rows at GQA 6) fits in 256 registers, which lets two workgroups share a CU;
 // NT = 2 (3-5 rows) needs the whole register file. Wider shapes use attn_partials_cols_kernel.
-template <int NT, int WAVES = waves_for<NT>()>
-__global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 2 : 1, 2)))
-attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
-                     const __bf16* __restrict__ vc, const int* __restrict__ pos_ptr,
-                     float* __restrict__ part_o, float* __restrict__ part_ml, int n, int Hq,
-                     int Hkv, int max_len, int NS, int CH, float scale_log2) {
+//
+// FUSED: the kernel also does qe_attn_prep's work (the q rows in registers come from qg through
+// the same RMSNorm1p + RoPE code, the new K/V rows are written to the cache), so prep + decode is
+// two launches. Each workgroup computes the q rows of its GQA group (slice 0 also writes q_out);
+// the workgroup whose slice holds position pos+t writes cache row pos+t before any of its waves
+// loads the tile holding it. Each wave issues its first tile's loads before the prep when that
+// tile holds no new row, so the prep runs while the cache streams in. kc/vc are written here, so
+// they are not __restrict__.
+template <int NT, bool FUSED = false, int WAVES = waves_for<NT>()>
+__global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_eu(NT == 1 && !FUSED ? 2 : 1, 2)))
+attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf16* vc,
+                     const int* __restrict__ pos_ptr, float* __restrict__ part_o,
+                     float* __restrict__ part_ml, int n, int Hq, int Hkv, int max_len, int NS,
+                     int CH, float scale_log2, PrepIn pin) {
   const int s = blockIdx.x, g = blockIdx.y;
   const int grp = Hq / Hkv;
   const int pos0 = pos_ptr[0];
   const int Lmax = min(pos0 + n, max_len);  // attended length of the last row
   const int beg = s * CH;
-  if (beg >= Lmax) return;  // slice holds no attended position (uniform per workgroup)
-  const int end = min(beg + CH, Lmax);
+  const bool attend = beg < Lmax;  // slice holds an attended position (uniform per workgroup)
+  if (!attend && !(FUSED && s == 0)) return;  // (slice 0 of the fused kernel still writes q_out)
+  const int end = max(min(beg + CH, Lmax), beg);
 
   const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
   const int c = lane & 15, g4 = lane >> 4;
@@ -131,6 +321,27 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc
   __shared__ __attribute__((aligned(16))) char lds[lds_k_bytes<WAVES>()];
   __shared__ float s_m[WAVES][16 * NT], s_l[WAVES][16 * NT];
   u32x4_t* ks_lds = reinterpret_cast<u32x4_t*>(lds) + w * TILE * ROW_CHUNKS;
+
+  const int Lmin = min(pos0 + 1, max_len);  // row 0 attends the fewest positions
+  const size_t head_off = (size_t)g * max_len * HD;
+  const uint32_t bytes = (uint32_t)max(end, 0) * (uint32_t)(HD * 2);  // loads past the slice read 0
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kc + head_off, bytes);
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vc + head_off, bytes);
+
+  int p0 = beg + w * TILE;  // this wave's first tile
+  VTile buf;
+  bool issued = false;
+  if constexpr (FUSED) {
+    // rows t in [t_lo, t_hi) sit at positions in this slice: their K/V rows are written here
+    const int t_lo = max(beg - pos0, 0);
+    const int t_hi = attend ? max(min(end - pos0, n), t_lo) : t_lo;  // empty when none is here
+    PrepRegs<NT> pr;
+    fused_prep_load<NT>(pr, pin, g, grp, n, ncols, t_lo, t_hi);
+    fused_prep_compute<NT>(pr, pin, s, g, grp, n, Hq, ncols, pos0, t_lo, t_hi, max_len,
+                           const_cast<__bf16*>(kc), const_cast<__bf16*>(vc),
+                           std::make_integer_sequence<int, PrepShape<NT>::MAXI>{});
+    if (!attend) return;  // slice 0 beyond every attended position: q_out written, nothing else
+  }
 
   // Q^T as the MFMA B operand. Column ct*16+c is (row t, head g*grp+j), col = t*grp + j.
   // Lane group g4 holds dims [32ks + 8g4, +8) of k-step ks (the same dims as the K operand).
@@ -142,22 +353,21 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc
     if (col < ncols) {
       const int t = col / grp, j = col - t * grp;
       Lcol[ct] = min(pos0 + t + 1, max_len);
-      const u32x4_t* src =
-          reinterpret_cast<const u32x4_t*>(q + (size_t)t * Hq * HD + (size_t)(g * grp + j) * HD);
+      if constexpr (FUSED) {
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) qb[ct][ks] = as_bf16x8(src[4 * ks + g4]);
+        for (int ks = 0; ks < 8; ++ks) qb[ct][ks] = as_bf16x8(fused_q_lds(col, 4 * ks + g4));
+      } else {
+        const u32x4_t* src =
+            reinterpret_cast<const u32x4_t*>(q + (size_t)t * Hq * HD + (size_t)(g * grp + j) * HD);
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) qb[ct][ks] = as_bf16x8(src[4 * ks + g4]);
+      }
     } else {
       Lcol[ct] = 0;  // padding column: every position masked
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) qb[ct][ks] = as_bf16x8(u32x4_t{0u, 0u, 0u, 0u});
     }
   }
-
-  const int Lmin = min(pos0 + 1, max_len);  // row 0 attends the fewest positions
-  const size_t head_off = (size_t)g * max_len * HD;
-  const uint32_t bytes = (uint32_t)end * (uint32_t)(HD * 2);  // loads past the slice read 0
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kc + head_off, bytes);
-  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vc + head_off, bytes);
 
   float m[NT], l[NT];
   f32x4_t acc[NT][16];  // [8hh + i]: O^T dims 128hh + 32g4 + 8ii + i (tile::pv_half)
@@ -169,9 +379,9 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc
     for (int a = 0; a < 16; ++a) acc[ct][a] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
-  for (int p0 = beg + w * TILE; p0 < end; p0 += WAVES * TILE) {
-    VTile buf;
-    load_tile(buf, ks_lds, krs, vrs, p0, lane, c, g4);
+  for (; p0 < end; p0 += WAVES * TILE) {
+    if (!issued) load_tile(buf, ks_lds, krs, vrs, p0, lane, c, g4);
+    issued = false;
     wait_and_compute<NT>(buf, ks_lds, p0, Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
   }
 
@@ -535,8 +745,8 @@ static hipError_t launch_partials(const void* q, const void* kc, const void* vc,
   // NT = 1, 2: every wave holds all column tiles (measured fastest at 1-5 rows, GQA 6).
   // NT = 3, 4: one subset wave per column tile (the one-tile kernel would spill: 2.3-2.8x slower).
   switch (NT) {
-    case 1: attn_partials_kernel<1><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
-    case 2: attn_partials_kernel<2><<<grid, dim3(waves_for<2>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
+    case 1: attn_partials_kernel<1><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2, PrepIn{}); break;
+    case 2: attn_partials_kernel<2><<<grid, dim3(waves_for<2>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2, PrepIn{}); break;
     case 3: attn_partials_cols_kernel<3, 1><<<grid, dim3(cols::SUBSETS * 3 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
     default: attn_partials_cols_kernel<4, 2><<<grid, dim3(cols::SUBSETS * 2 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
   }
@@ -589,6 +799,57 @@ extern "C" hipError_t qe_attn_decode(const void* q, const void* kc, const void* 
                                      int NS, float scale, hipStream_t stream) {
   hipError_t e = qe_attn_decode_partials(q, kc, vc, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS,
                                          scale, stream);
+  if (e != hipSuccess) return e;
+  return qe_attn_decode_combine(part_o, part_ml, pos, qg, ldp, out, ldo, n, Hq, max_len, NS,
+                                stream);
+}
+
+extern "C" hipError_t qe_attn_prep(const void* qg, const void* k, const void* v, long ldp,
+                                   const void* qnw, const void* knw, const float* inv_freq,
+                                   const int* pos, void* q_out, void* kc, void* vc, int n, int Hq,
+                                   int Hkv, int max_len, int rd, float eps, hipStream_t stream);
+
+extern "C" hipError_t qe_attn_prep_decode(const void* qg, const void* k, const void* v, long ldp,
+                                          const void* qnw, const void* knw, const float* inv_freq,
+                                          const int* pos, void* q_out, void* kc, void* vc,
+                                          float* part_o, float* part_ml, void* out, long ldo,
+                                          int n, int Hq, int Hkv, int max_len, int rd, int NS,
+                                          float scale, float eps, hipStream_t stream) {
+  hipError_t e = check_decode_shape(n, Hq, Hkv, max_len, NS);
+  if (e != hipSuccess) return e;
+  if (rd < 0 || rd > HD || (rd & 1) || ldp < 1 || !qg || !k || !v || !qnw || !knw ||
+      !inv_freq || !pos || !q_out || !kc || !vc || !part_o || !part_ml || !out)
+    return hipErrorInvalidValue;
+  if (!aligned16(q_out) || !aligned16(kc) || !aligned16(vc) || !aligned16(part_o))
+    return hipErrorInvalidValue;
+  const int NT = ((Hq / Hkv) * n + 15) / 16;
+  // Wide verify shapes, rotary parts with more table entries than threads or not a multiple of 8
+  // dims, and input rows the 16-byte loads cannot read: the prep kernel, then the decode.
+  if (NT > 2 || rd == 0 || rd % 8 != 0 || n * (rd / 2) > ROPE_TAB || ldp % 8 != 0 ||
+      !aligned16(qg) || !aligned16(k) || !aligned16(qnw) || !aligned16(knw) ||
+      !aligned16(inv_freq)) {
+    e = qe_attn_prep(qg, k, v, ldp, qnw, knw, inv_freq, pos, q_out, kc, vc, n, Hq, Hkv, max_len,
+                     rd, eps, stream);
+    if (e != hipSuccess) return e;
+    return qe_attn_decode(q_out, kc, vc, pos, qg, ldp, part_o, part_ml, out, ldo, n, Hq, Hkv,
+                          max_len, NS, scale, stream);
+  }
+  const int CH = split_size(max_len, NS);
+  const dim3 grid((max_len + CH - 1) / CH, Hkv);
+  const PrepIn pin{static_cast<const __bf16*>(qg), static_cast<const __bf16*>(k),
+                   static_cast<const __bf16*>(v), ldp, static_cast<const __bf16*>(qnw),
+                   static_cast<const __bf16*>(knw), inv_freq, static_cast<__bf16*>(q_out), rd,
+                   eps};
+  const float scale_log2 = scale * 1.4426950408889634f;
+  const auto* K = static_cast<const __bf16*>(kc);
+  const auto* V = static_cast<const __bf16*>(vc);
+  if (NT == 1)
+    attn_partials_kernel<1, true><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(
+        nullptr, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2, pin);
+  else
+    attn_partials_kernel<2, true><<<grid, dim3(waves_for<2>() * WAVE), 0, stream>>>(
+        nullptr, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2, pin);
+  e = hipGetLastError();
   if (e != hipSuccess) return e;
   return qe_attn_decode_combine(part_o, part_ml, pos, qg, ldp, out, ldo, n, Hq, max_len, NS,
                                 stream);

@@ -3,9 +3,9 @@
 // q_out and k/v to the KV cache. Semantics: reference csrc/attn.cu:17-56 and
 // python/qengine/reference.py:132-136,158-176,252-260.
 //
-// One 256-thread workgroup per (head, row): thread c owns dim c. The sum of squares is a wave64
-// shuffle reduction plus a fixed-order sum of the four wave partials. The rotate-half partner
-// comes through LDS. The op is a few KB per row and launch-latency bound.
+// One 256-thread workgroup per (head, row): thread c owns dim c (qe::prep_dim, shared with the
+// fused prep + decode kernel so both produce the same bits). The op is a few KB per row and
+// launch-latency bound.
 #include "qe_device.hpp"
 #include "qe_attn.h"
 
@@ -27,28 +27,8 @@ attn_prep_kernel(const __bf16* __restrict__ qg, const __bf16* __restrict__ k,
   const size_t row = (size_t)t * ldp;
 
   const float x = bf16_to_f32(is_q ? qg[row + (size_t)h * 2 * HD + c] : k[row + (size_t)h * HD + c]);
-  const float sq = wave_sum(x * x);
-  if ((c & (WAVE - 1)) == 0) red[c / WAVE] = sq;
-  __syncthreads();
-  const float total = ((red[0] + red[1]) + red[2]) + red[3];
-  const float inv = 1.0f / sqrtf(total / (float)HD + eps);
   const float wgt = bf16_to_f32(is_q ? qnw[c] : knw[c]);
-  const float xv = round_bf16((x * inv) * (1.0f + wgt));  // RMSNorm1p output is a bf16 tensor
-  xn[c] = xv;
-  __syncthreads();
-
-  float y = xv;
-  if (c < rd) {
-    const int half = rd >> 1;
-    const float ang = (float)pos * inv_freq[c < half ? c : c - half];  // fp32 angle
-    // cos/sin of the fp32 angle evaluated in fp64 and rounded once: the correctly rounded fp32
-    // value, which is what the reference's fp32 cos/sin return in all but rare cases (single
-    // precision device cos/sin can be a couple of ulps off, enough to flip a bf16 rounding).
-    const double angd = (double)ang;
-    const float cs = round_bf16((float)cos(angd)), sn = round_bf16((float)sin(angd));
-    const float rot = c < half ? -xn[c + half] : xn[c - half];  // rotate_half
-    y = round_bf16(round_bf16(xv * cs) + round_bf16(rot * sn));
-  }
+  const float y = prep_dim(x, wgt, rope_cs(pos, inv_freq, rd, c), rd, eps, xn, red);
   if (is_q) {
     q_out[(size_t)t * Hq * HD + (size_t)h * HD + c] = f32_to_bf16(y);
   } else if (pos >= 0 && pos < max_len) {  // never write outside the cache

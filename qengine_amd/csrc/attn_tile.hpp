@@ -124,27 +124,5 @@ __device__ __forceinline__ void pv_half(const u32x4_t (&vr)[8], int hh, const u3
   }
 }
 
-// O^T += V^T P^T for one 64-dim quarter of V (the decode layout): vr[e] = 8 bytes of V row
-// P(g4, e), quarter dims 4c + [0, 4). M-tile mt has row c = quarter dim 4c + mt, so
-// acc[ct][mt][i] = O^T[quarter dim 16g4 + 4i + mt][column c]: each lane ends up holding 16
-// consecutive dims (16g4 + [0, 16)) of its column.
-template <int NT, bool SPLIT>
-__device__ __forceinline__ void pv_quarter(const u32x2_t (&vr)[8], const u32x4_t (&pb_hi)[NT],
-                                           const u32x4_t (&pb_lo)[NT], f32x4_t (&acc)[NT][4]) {
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    u32x4_t a;
-#pragma unroll
-    for (int d = 0; d < 4; ++d)
-      a[d] = interleave_halves(vr[2 * d][mt >> 1], vr[2 * d + 1][mt >> 1], mt & 1);
-#pragma unroll
-    for (int ct = 0; ct < NT; ++ct) {
-      acc[ct][mt] = mfma16x16x32(as_bf16x8(a), as_bf16x8(pb_hi[ct]), acc[ct][mt]);
-      if constexpr (SPLIT)
-        acc[ct][mt] = mfma16x16x32(as_bf16x8(a), as_bf16x8(pb_lo[ct]), acc[ct][mt]);
-    }
-  }
-}
-
 }  // namespace tile
 }  // namespace qe

@@ -196,6 +196,24 @@ void attn_decode(torch::Tensor q, torch::Tensor kc, torch::Tensor vc, torch::Ten
            "qe_attn_decode");
 }
 
+// attn_prep then attn_decode (q_out is the decode's q) in two launches: the split-KV kernel
+// computes its q rows and writes the new cache rows itself. Bit-identical to the two calls.
+void attn_prep_decode(torch::Tensor qg, torch::Tensor k, torch::Tensor v, torch::Tensor qnw,
+                      torch::Tensor knw, torch::Tensor inv_freq, torch::Tensor pos,
+                      torch::Tensor q_out, torch::Tensor kc, torch::Tensor vc, double eps,
+                      torch::Tensor part_o, torch::Tensor part_ml, torch::Tensor out) {
+  const auto a = parse_prep(qg, k, v, qnw, knw, inv_freq, pos, q_out, kc, vc, true);
+  const auto d = parse_decode(q_out, kc, vc, pos, qg, part_o, part_ml, out, true);
+  const c10::DeviceGuard guard(qg.device());
+  raise_on(qe_attn_prep_decode(qg.data_ptr(), k.data_ptr(), v.data_ptr(), a.ldp, qnw.data_ptr(),
+                               knw.data_ptr(), inv_freq.data_ptr<float>(), pos.data_ptr<int>(),
+                               q_out.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                               part_o.data_ptr<float>(), part_ml.data_ptr<float>(),
+                               out.data_ptr(), d.ldo, a.n, a.Hq, a.Hkv, a.max_len, a.rd, d.NS,
+                               1.0f / 16.0f, (float)eps, stream_of(qg)),
+           "qe_attn_prep_decode");
+}
+
 // The two halves of attn_decode (same arguments): split-KV partials, then the gated combine.
 void attn_decode_partials(torch::Tensor q, torch::Tensor kc, torch::Tensor vc, torch::Tensor pos,
                           torch::Tensor qg, torch::Tensor part_o, torch::Tensor part_ml,
@@ -228,6 +246,17 @@ std::vector<int64_t> check_attn_prep(torch::Tensor qg, torch::Tensor k, torch::T
   return {a.n, a.Hq, a.Hkv, a.max_len, a.rd, a.ldp};
 }
 
+std::vector<int64_t> check_attn_prep_decode(torch::Tensor qg, torch::Tensor k, torch::Tensor v,
+                                            torch::Tensor qnw, torch::Tensor knw,
+                                            torch::Tensor inv_freq, torch::Tensor pos,
+                                            torch::Tensor q_out, torch::Tensor kc, torch::Tensor vc,
+                                            torch::Tensor part_o, torch::Tensor part_ml,
+                                            torch::Tensor out) {
+  const auto a = parse_prep(qg, k, v, qnw, knw, inv_freq, pos, q_out, kc, vc, false);
+  const auto d = parse_decode(q_out, kc, vc, pos, qg, part_o, part_ml, out, false);
+  return {a.n, a.Hq, a.Hkv, a.max_len, a.rd, a.ldp, d.NS, d.ldo};
+}
+
 std::vector<int64_t> check_attn_decode(torch::Tensor q, torch::Tensor kc, torch::Tensor vc,
                                        torch::Tensor pos, torch::Tensor qg, torch::Tensor part_o,
                                        torch::Tensor part_ml, torch::Tensor out) {
@@ -243,6 +272,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "split-KV partials of attn_decode (same arguments)");
   m.def("attn_decode_combine", &attn_decode_combine,
         "log-sum-exp combine + sigmoid gate of attn_decode (same arguments)");
+  m.def("attn_prep_decode", &attn_prep_decode,
+        "attn_prep then attn_decode in two launches (qg, k, v, qnw, knw, inv_freq, pos, q_out, kc, "
+        "vc, eps, part_o, part_ml, out)");
   m.def("attn_prep_chunk", &attn_prep_chunk, "attn_prep without the 8-row limit (prefill chunks)");
   m.def("attn_prefill", &attn_prefill,
         "chunked-prefill gated attention over the KV cache (q, kc, vc, pos, qg, out)");
@@ -254,6 +286,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("set_pdl_launch", [](bool on) { qe_set_pdl_launch(on); },
         "no-op on gfx950 (kept for import compatibility)");
   m.def("_check_attn_prep", &check_attn_prep, "validate attn_prep arguments without launching");
+  m.def("_check_attn_prep_decode", &check_attn_prep_decode,
+        "validate attn_prep_decode arguments without launching");
   m.def("_check_attn_decode", &check_attn_decode,
         "validate attn_decode arguments without launching");
 }

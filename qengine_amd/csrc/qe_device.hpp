@@ -12,7 +12,6 @@ constexpr int WAVE = 64;     // CDNA wavefront
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------- bf16 rounding
 // torch rounds every bf16 op result to nearest-even; these model one such rounding.
@@ -46,6 +45,25 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// wave_sum with the same pairing (xor 32, 16, 8, 4, 2, 1; each level adds the partner lane's
+// value) on VALU lane moves instead of LDS-crossbar permutes, so it returns the same bits at a
+// fraction of the latency: xor 32/16 by the gfx950 permlane swaps, xor 8 by DPP row_ror:8, xor 4
+// by DPP row_half_mirror then quad_perm [3,2,1,0], xor 2 and 1 by DPP quad_perm.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __uint_as_float(__builtin_amdgcn_mov_dpp(__float_as_uint(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_fast(float v) {
+  auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+  auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+  v = v + dpp<0x128>(v);              // row_ror:8 = lane ^ 8 within 16
+  v = v + dpp<0x1B>(dpp<0x141>(v));   // row_half_mirror, then quad_perm [3,2,1,0]: lane ^ 4
+  v = v + dpp<0x4E>(v);               // quad_perm [2,3,0,1]: lane ^ 2
+  return v + dpp<0xB1>(v);            // quad_perm [1,0,3,2]: lane ^ 1
+}
+
 // Max / sum across the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48) with the gfx950
 // VALU lane swaps instead of an LDS-crossbar permute. permlane16_swap(v, v) returns, per lane,
 // the values of 16-lane rows (0,0,2,2) and (1,1,3,3); permlane32_swap(v, v) returns the low and
@@ -65,6 +83,65 @@ __device__ __forceinline__ float xor32_pair(float v, bool sum) {
 }
 __device__ __forceinline__ float group4_max(float v) { return xor32_pair(xor16_pair(v, false), false); }
 __device__ __forceinline__ float group4_sum(float v) { return xor32_pair(xor16_pair(v, true), true); }
+
+// ---------------------------------------------------------------------------- q/k prep
+// RMSNorm1p + partial rotate-half RoPE of one 256-dim row with a 256-thread workgroup, thread c
+// owning dim c (reference csrc/attn.cu:37-49, python/qengine/reference.py:132-136,158-176):
+// y = bf16(bf16(xn*cos) + bf16(rot(xn)*sin)) on dims < rd, xn = bf16(x * rsqrt(mean x^2 + eps) *
+// (1 + w)); cos/sin of the fp32 angle pos*inv_freq rounded to bf16. Shared by the prep kernel and
+// the fused prep + decode kernel, so both produce the same bits.
+
+// cos/sin of thread c's rotary angle at position pos ({1, 0} for dims >= rd). Evaluated in fp64
+// from the fp32 angle and rounded once: the correctly rounded fp32 value, which is what the
+// reference's fp32 cos/sin return in all but rare cases (single-precision device cos/sin can be a
+// couple of ulps off, enough to flip a bf16 rounding).
+struct RopeCS {
+  float cs, sn;
+};
+// Thread c's rotary frequency (0 for dims >= rd).
+__device__ __forceinline__ float rope_freq(const float* __restrict__ inv_freq, int rd, int c) {
+  const int half = rd >> 1;
+  return c < rd ? inv_freq[c < half ? c : c - half] : 0.f;
+}
+__device__ __forceinline__ RopeCS rope_cs_f(int pos, float freq, int rd, int c) {
+  if (c >= rd) return {1.f, 0.f};
+  const double angd = (double)((float)pos * freq);  // the fp32 angle, in fp64
+  return {round_bf16((float)cos(angd)), round_bf16((float)sin(angd))};
+}
+__device__ __forceinline__ RopeCS rope_cs(int pos, const float* __restrict__ inv_freq, int rd,
+                                          int c) {
+  return rope_cs_f(pos, rope_freq(inv_freq, rd, c), rd, c);
+}
+
+// Workgroup barrier for LDS data only: this wave's LDS writes have landed (lgkmcnt(0)), then
+// s_barrier between compiler fences. Outstanding global loads stay in flight (unlike
+// __syncthreads(), whose release waits for every vector-memory operation).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt at their maxima
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The sum of squares is a wave64 butterfly plus a fixed-order sum of the four wave partials. xn
+// (256 floats) and red (4 floats) are LDS scratch. Contains two workgroup barriers (LDS only):
+// every thread of the workgroup calls it, the same number of times.
+__device__ __forceinline__ float prep_dim(float x, float wgt, RopeCS r, int rd, float eps,
+                                          float* xn, float* red) {
+  const int c = threadIdx.x;
+  const float sq = wave_sum_fast(x * x);
+  if ((c & (WAVE - 1)) == 0) red[c / WAVE] = sq;
+  lds_barrier();
+  const float total = ((red[0] + red[1]) + red[2]) + red[3];
+  const float inv = 1.0f / sqrtf(total / (float)HD + eps);
+  const float xv = round_bf16((x * inv) * (1.0f + wgt));  // RMSNorm1p output is a bf16 tensor
+  xn[c] = xv;
+  lds_barrier();
+  if (c >= rd) return xv;
+  const int half = rd >> 1;
+  const float rot = c < half ? -xn[c + half] : xn[c - half];  // rotate_half
+  return round_bf16(round_bf16(xv * r.cs) + round_bf16(rot * r.sn));
+}
 
 // ---------------------------------------------------------------------------- buffer loads
 // Raw buffer resource over [base, base + bytes). Loads whose dword lies past `bytes` return 0

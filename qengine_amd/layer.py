@@ -6,8 +6,11 @@ The reference runs, per full-attention layer and pass of n rows (python/qengine/
   attn_decode(q, kc, vc, pos, pr[:, :q0], part_o, part_ml, out)
 with inv_freq built on the CPU in fp32 and moved (engine.py:409-410), per-layer kc/vc
 [Hkv, max_len, 256] (engine.py:419) and a shared q / part_o / part_ml scratch (engine.py:405-408).
-GatedAttention owns the same buffers and issues the same two calls. It allocates only at
-construction, so a pass can be captured in a hipGraph.
+GatedAttention owns the same buffers and issues the same work, by default as the reference's two
+calls; fused=True issues the fused attn_prep_decode instead (two launches instead of three,
+bit-identical results, but about 1 us slower per layer-call on gfx950 because the prep phase
+delays every workgroup's first KV tile). It allocates only at construction, so a pass can be
+captured in a hipGraph.
 """
 from __future__ import annotations
 
@@ -30,9 +33,9 @@ class GatedAttention:
 
     def __init__(self, hq: int, hkv: int, max_len: int, q_norm: torch.Tensor, k_norm: torch.Tensor,
                  rope_theta: float = 1e7, rotary_dim: int = 64, eps: float = 1e-6, n_max: int = 8,
-                 splits: int | None = None, device="cuda"):
+                 splits: int | None = None, fused: bool = False, device="cuda"):
         d = HEAD_DIM
-        self.hq, self.hkv, self.max_len, self.eps = hq, hkv, max_len, eps
+        self.hq, self.hkv, self.max_len, self.eps, self.fused = hq, hkv, max_len, eps, fused
         self.q_norm, self.k_norm = q_norm.to(device), k_norm.to(device)
         self.inv_freq = rope_inv_freq(rope_theta, rotary_dim, device)
         self.kc = torch.zeros(hkv, max_len, d, dtype=torch.bfloat16, device=device)
@@ -52,7 +55,11 @@ class GatedAttention:
         pr = proj[:, : self.width]
         qg = pr[:, : self.q0]
         q = self.q[:n]
-        _C.attn_prep(qg, pr[:, self.q0: self.k1], pr[:, self.k1:], self.q_norm, self.k_norm,
-                     self.inv_freq, pos, q, self.kc, self.vc, self.eps)
-        _C.attn_decode(q, self.kc, self.vc, pos, qg, self.part_o, self.part_ml, out)
+        prep = (qg, pr[:, self.q0: self.k1], pr[:, self.k1:], self.q_norm, self.k_norm,
+                self.inv_freq, pos, q, self.kc, self.vc, self.eps)
+        if self.fused:
+            _C.attn_prep_decode(*prep, self.part_o, self.part_ml, out)
+        else:
+            _C.attn_prep(*prep)
+            _C.attn_decode(q, self.kc, self.vc, pos, qg, self.part_o, self.part_ml, out)
         return out

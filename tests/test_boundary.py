@@ -82,6 +82,24 @@ def test_capi_prep_rejects(capi, kw, why):
     assert r == INVALID, why
 
 
+@pytest.mark.parametrize("kw,why", [
+    (dict(n=0), "no rows"), (dict(n=9), "more than 8 rows"), (dict(rd=3), "odd rotary dims"),
+    (dict(hq=25), "Hq % Hkv"), (dict(ns=0), "no splits"), (dict(q_out=A + 8), "unaligned q_out"),
+    (dict(qg=None), "null qg"), (dict(out=None), "null out"),
+    (dict(max_len=1 << 23), "cache beyond 32-bit buffer offsets"),
+])
+def test_capi_prep_decode_rejects(capi, kw, why):
+    a = dict(qg=A, k=A, v=A, ldp=24 * 512 + 2048, qnw=A, knw=A, inv=A, pos=A, q_out=A, kc=A,
+             vc=A, part_o=A, part_ml=A, out=A, ldo=24 * D, n=1, hq=24, hkv=4, max_len=4096, rd=64,
+             ns=16)
+    a.update(kw)
+    r = capi.load().qe_attn_prep_decode(
+        a["qg"], a["k"], a["v"], a["ldp"], a["qnw"], a["knw"], a["inv"], a["pos"], a["q_out"],
+        a["kc"], a["vc"], a["part_o"], a["part_ml"], a["out"], a["ldo"], a["n"], a["hq"],
+        a["hkv"], a["max_len"], a["rd"], a["ns"], 1.0 / 16, 1e-6, None)
+    assert r == INVALID, why
+
+
 def test_pdl_switches_are_noops(native):
     native.set_pdl_trigger(True)
     native.set_pdl_launch(False)
@@ -198,3 +216,24 @@ def test_prep_contract_rejects(native, mutate, msg):
 def test_prep_contract_row_limit(native):
     with pytest.raises(RuntimeError, match="1..8 rows"):
         check_prep(native, prep_args(n=9))
+
+
+def test_prep_decode_contract(native):
+    """attn_prep_decode validates as attn_prep (on qg, k, v, ..., q_out, kc, vc) and as
+    attn_decode (with q_out as q) together."""
+    C = native
+    n, hq, hkv, max_len, ns = 3, 24, 4, 64, 4
+    a = decode_args(n=n, hq=hq, hkv=hkv, max_len=max_len, ns=ns)
+    proj = torch.zeros(n, hq * 2 * D + 2 * hkv * D + 8, dtype=BF)
+    qg, k, v = (proj[:, : hq * 2 * D], proj[:, hq * 2 * D: hq * 2 * D + hkv * D],
+                proj[:, hq * 2 * D + hkv * D: hq * 2 * D + 2 * hkv * D])
+    qnw, knw, inv = torch.zeros(D, dtype=BF), torch.zeros(D, dtype=BF), torch.zeros(32, dtype=F32)
+    res = C._check_attn_prep_decode(qg, k, v, qnw, knw, inv, a["pos"], a["q"], a["kc"], a["vc"],
+                                    a["part_o"], a["part_ml"], a["out"])
+    assert list(res[:5]) == [n, hq, hkv, max_len, 64] and res[6] == ns
+    with pytest.raises(RuntimeError, match="part_o"):
+        C._check_attn_prep_decode(qg, k, v, qnw, knw, inv, a["pos"], a["q"], a["kc"], a["vc"],
+                                  a["part_o"][:, :, :, :128], a["part_ml"], a["out"])
+    with pytest.raises(RuntimeError, match="rows"):
+        C._check_attn_prep_decode(qg[:2], k[:2], v[:2], qnw, knw, inv, a["pos"], a["q"][:2],
+                                  a["kc"], a["vc"], a["part_o"], a["part_ml"], a["out"])
