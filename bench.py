@@ -245,6 +245,27 @@ def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
                      "hbm_frac": round(alg_bytes_layer(L) / (us * 1e3) / HBM_PEAK_GBS, 4)}
     del kcs, vcs
 
+    # one row attending 4096 positions of 131072-position caches (a cache sized for long context,
+    # early in a generation), 16 layers: the slices follow the attended length, so this runs like
+    # the 4096-position sweep entry, not like a 131072-position cache cut into fixed slices
+    Lc, La, nl = 131072, 4096, 16
+    kcs = [torch.empty(HKV, Lc, D, dtype=BF, device=dev) for _ in range(nl)]
+    vcs = [torch.empty(HKV, Lc, D, dtype=BF, device=dev) for _ in range(nl)]
+    for kk, vv in zip(kcs, vcs):
+        kk[:, :La] = rnd(HKV, La, D)
+        vv[:, :La] = rnd(HKV, La, D)
+    ns = qa.default_splits(Lc, HKV)
+    poc, pmlc = qa.alloc_partials(1, HQ, ns, dev)
+    posc = torch.tensor([La - 1], dtype=torch.int32, device=dev)
+
+    def short_in_long():
+        for kk, vv in zip(kcs, vcs):
+            C.attn_decode(q1, kk, vv, posc, qg1, poc, pmlc, out)
+    us = time_fn_graph(torch, short_in_long, steps, warmup) * 1e3 / nl
+    res["decode_4k_in_128k_cache"] = {"us_per_layer": round(us, 3),
+                                      "GBps": round(alg_bytes_layer(La) / (us * 1e3), 1)}
+    del kcs, vcs
+
     res.update(bench_prefill(torch, C, steps, warmup))
     return res
 

@@ -41,9 +41,10 @@ hipError_t qe_attn_prep(const void* qg, const void* k, const void* v, long ldp, 
 
 /* Gated flash-decoding: row t attends cache positions [0, min(pos+t+1, max_len)), scores scaled
  * by `scale`, and out[t] = bf16(bf16(softmax . V) * bf16(sigmoid(gate))), gate = qg[t][h][D:2D].
- * Two launches: split-KV partials over fixed slices of qe_attn_split_size(max_len, NS)
- * positions, then a log-sum-exp combine with the fused sigmoid gate. Row t of an n-row call is
- * bit-identical to a 1-row call at position pos+t. Valid: 1 <= n <= 8, Hq % Hkv == 0,
+ * Two launches: split-KV partials, row t over slices of qe_attn_split_size(L_t, NS) positions
+ * (L_t = min(pos+t+1, max_len), so about NS slices hold work whatever max_len is), then a
+ * log-sum-exp combine with the fused sigmoid gate. Row t of an n-row call is bit-identical to a
+ * 1-row call at position pos+t. Valid: 1 <= n <= 8, Hq % Hkv == 0,
  * (Hq/Hkv)*n <= 64, NS >= 1, (max_len+32)*512 < 2^32, 16-byte aligned q/kc/vc/part_o.
  * Replaces launch_attn_decode (reference csrc/ops.h:28-30, csrc/attn.cu:165-172). */
 hipError_t qe_attn_decode(const void* q, const void* kc, const void* vc, const int* pos,
@@ -92,11 +93,12 @@ hipError_t qe_attn_prefill(const void* q, const void* kc, const void* vc, const 
                            const void* qg, long ldp, void* out, long ldo, int T, int Hq, int Hkv,
                            int max_len, float scale, hipStream_t stream);
 
-/* Number of cache positions per split-KV slice for a cache of max_len positions and NS partial
- * slots: a multiple of 32, at least ceil(max_len/NS). It depends only on (max_len, NS), so the
- * slices are the same for every row and every call on the same buffers.
- * No counterpart in the reference (its slice size depends on each row's length, attn.cu:79). */
-int qe_attn_split_size(int max_len, int NS);
+/* Number of cache positions per split-KV slice for a row attending L positions with NS partial
+ * slots: ceil(L/NS) rounded up to a multiple of 32 (at least 32); row t's partial s covers
+ * positions [s*size, (s+1)*size) of [0, L). The reference cuts ceil(L/NS) (csrc/attn.cu:78-80);
+ * this function has no counterpart there. It runs the kernels' own arithmetic (a host-computed
+ * multiply and shift for the division by NS). Returns 0 for L < 1, L >= 2^23 or NS < 1. */
+int qe_attn_split_size(int L, int NS);
 
 /* Version string of this library. */
 const char* qe_attn_version(void);

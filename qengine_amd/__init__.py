@@ -51,9 +51,8 @@ def default_splits(max_len: int, hkv: int = 4, cus: int | None = None) -> int:
     compute unit when the whole cache is attended (NS * Hkv = CUs), never slices shorter than
     32 positions. Measured on MI355X, this is the fastest choice from 4k to 128k positions:
     fewer slices leave CUs idle, more slices cost a second round of workgroups and more partials.
-    NS is fixed when the scratch is allocated, so graphs stay static; the slice size
-    split_size(max_len, NS) depends on max_len, so a cache much longer than the attended prefix
-    leaves most slices empty (they exit at once) and fewer CUs busy."""
+    NS is fixed when the scratch is allocated, so graphs stay static; a row attending L
+    positions uses slices of split_size(L, NS), so about NS slices hold work at every length."""
     cus = cus or compute_units()
     return max(1, min(math.ceil(max_len / MIN_SLICE), max(1, cus // hkv)))
 

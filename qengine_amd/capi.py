@@ -107,8 +107,9 @@ def prefill(q, kc, vc, pos, qg, ldp, out, ldo, T, hq, hkv, max_len, scale=1.0 / 
                                   ldo, T, hq, hkv, max_len, scale, _stream(stream))
 
 
-def split_size(max_len: int, ns: int) -> int:
-    return load().qe_attn_split_size(max_len, ns)
+def split_size(L: int, ns: int) -> int:
+    """Slice size of a row attending L positions with ns partial slots (qe_attn_split_size)."""
+    return load().qe_attn_split_size(L, ns)
 
 
 def version() -> str:

@@ -5,9 +5,13 @@
 // bf16(bf16(softmax . V) * bf16(sigmoid(gate))).
 //
 // Design (MI355X-first, not a translation of the reference's warp-per-position loop):
-//  * One workgroup per (split-KV slice, KV head). The slice size CH depends only on (max_len,
-//    NS), so every row of every call sees the same slices: row t of an n-row call is
-//    bit-identical to a 1-row call at position pos+t, and rows can share each K/V tile.
+//  * One workgroup per (split-KV slice, KV head). Row t attends L_t positions, cut into slices of
+//    split_size(L_t, NS) positions (the reference cuts ceil(L_t/NS), attn.cu:78-80; here that is
+//    rounded up to whole 32-position tiles), so about NS slices hold work whatever the cache
+//    capacity. A row's slices depend on its own length only: row t of an n-row call is
+//    bit-identical to a 1-row call at position pos+t. The n <= 8 rows of a call use at most two
+//    slice sizes; rows of one size share each K/V tile, and a call whose rows straddle a size
+//    change runs one pass per size.
 //  * The Hq/Hkv query heads of the GQA group times the n rows form the columns of the MFMA tiles
 //    (NT tiles of 16 columns). K and V are read from HBM exactly once per call; Q stays in
 //    registers as an MFMA operand.
@@ -39,10 +43,74 @@ template <int NT>
 constexpr int waves_for() { return 4; }
 using tile::ROW_CHUNKS;
 
-__host__ __device__ inline int split_size(int max_len, int NS) {
-  long per = ((long)max_len + NS - 1) / NS;
-  per = (per + TILE - 1) / TILE * TILE;
-  return per < TILE ? TILE : (int)per;
+// Division by NS as a multiply and a shift, computed once on the host (Granlund & Montgomery,
+// "Division by invariant integers using multiplication", 1994, Thm 4.2): with l = ceil(log2 NS)
+// and m = floor(2^(23+l) / NS) + 1, floor(a / NS) == (a * m) >> (23 + l) for 0 <= a < 2^23.
+// Cache lengths stay below 2^23 (the 32-bit buffer range), so every slicing division is exact;
+// the kernels do it in a few scalar instructions instead of a reciprocal-based division.
+struct NsDiv {
+  uint32_t m;
+  int sh;
+};
+inline NsDiv ns_div(int NS) {
+  int l = 0;
+  while ((1ll << l) < NS) ++l;
+  return NsDiv{(uint32_t)((1ull << (23 + l)) / (unsigned long long)NS + 1), 23 + l};
+}
+constexpr int SPLIT_L_MAX = 1 << 23;  // split_size's range for L
+
+// Slice size for a row attending L positions (1 <= L < 2^23): ceil(L/NS) rounded up to whole
+// tiles.
+__host__ __device__ inline int split_size(int L, NsDiv d) {
+  if (L < 1) return TILE;
+  const uint32_t per = (uint32_t)(((unsigned long long)(uint32_t)(L - 1) * d.m) >> d.sh) + 1u;
+  return (int)((per + TILE - 1) / TILE * TILE);
+}
+
+// One pass of a workgroup: rows [r0, r1) of the call share the slice size ch; this workgroup's
+// slice s of them is [beg, end) (empty when beg >= end). Lmin is row r0's attended length.
+struct Pass {
+  int r0, r1, ch, beg, end, Lmin;
+};
+
+__device__ __forceinline__ Pass make_pass(int r0, int r1, int ch, int pos0, int max_len, int s) {
+  Pass P;
+  P.r0 = r0;
+  P.r1 = r1;
+  P.ch = ch;
+  P.Lmin = min(pos0 + r0 + 1, max_len);
+  const int Lhi = min(pos0 + r1, max_len);
+  P.beg = s * ch;
+  P.end = min(P.beg + ch, Lhi);
+  return P;
+}
+
+// The call's passes: rows [0, tB) use slices of ch0 = split_size(L_0, NS) positions, rows [tB, n)
+// slices of ch0 + 32. split_size(L) == ch0 exactly while L <= ch0 * NS, and n <= 8 consecutive
+// lengths never reach a third size, so one division serves the whole call. Uniform.
+__device__ __forceinline__ void call_split(int pos0, int n, int max_len, int NS, NsDiv nd,
+                                           int& ch0, int& tB) {
+  ch0 = split_size(min(pos0 + 1, max_len), nd);
+  const long long lim = (long long)ch0 * NS;  // longest length with slices of ch0
+  tB = n;
+  if (max_len > lim && pos0 + n > lim) tB = (int)(lim - pos0);  // row tB is the first past lim
+}
+
+__device__ __forceinline__ Pass pass_of(int pi, int ch0, int tB, int n, int pos0, int max_len,
+                                        int s) {
+  return pi == 0 ? make_pass(0, tB, ch0, pos0, max_len, s)
+                 : make_pass(tB, n, ch0 + TILE, pos0, max_len, s);
+}
+
+// Column col = t*grp + j (row t) belongs to the pass: its partial is stored.
+__device__ __forceinline__ bool in_pass(int col, int grp, const Pass& P) {
+  return col >= P.r0 * grp && col < P.r1 * grp;
+}
+
+// Slices that can hold work: a row attends at most max_len positions, in slices of >= 32.
+static inline int max_slices(int max_len, int NS) {
+  const int tiles = (max_len + TILE - 1) / TILE;
+  return NS < tiles ? NS : tiles;
 }
 
 // Registers of one wave step (32 cache positions of one KV head). K goes straight to LDS.
@@ -291,167 +359,187 @@ __device__ __forceinline__ void fused_prep_compute(const PrepRegs<NT>& r, const 
 // part_o [n][Hq][NS][HD] (unnormalised O), part_ml [n][Hq][NS][2] = (max in log2 units, sum).
 // NT = 1 (decode, 1-2 rows at GQA 6) fits in 256 registers, which lets two workgroups share a CU;
 // NT = 2 (3-5 rows) needs the whole register file. Wider shapes use attn_partials_cols_kernel.
+// Columns of rows outside the current pass are computed along (columns never mix) and not stored.
 //
 // FUSED: the kernel also does qe_attn_prep's work (the q rows in registers come from qg through
 // the same RMSNorm1p + RoPE code, the new K/V rows are written to the cache), so prep + decode is
-// two launches. Each workgroup computes the q rows of its GQA group (slice 0 also writes q_out);
-// the workgroup whose slice holds position pos+t writes cache row pos+t before any of its waves
-// loads the tile holding it. Each wave issues its first tile's loads before the prep when that
-// tile holds no new row, so the prep runs while the cache streams in. kc/vc are written here, so
-// they are not __restrict__.
-template <int NT, bool FUSED = false, int WAVES = waves_for<NT>()>
+// two launches. Each workgroup computes the q rows of its GQA group (slice 0 also writes q_out).
+// Every workgroup whose slices hold a position pos+t writes cache row pos+t itself, before any of
+// its waves loads a tile, so it never depends on another workgroup's write (when two workgroups
+// write one row, they write the same bits). kc/vc are written here, so they are not __restrict__.
+template <int NT, bool FUSED = false, bool MULTI = true, int WAVES = waves_for<NT>()>
 __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_eu(NT == 1 && !FUSED ? 2 : 1, 2)))
 attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf16* vc,
                      const int* __restrict__ pos_ptr, float* __restrict__ part_o,
                      float* __restrict__ part_ml, int n, int Hq, int Hkv, int max_len, int NS,
-                     int CH, float scale_log2, PrepIn pin) {
+                     NsDiv nd, float scale_log2, PrepIn pin) {
+  const int pos0 = pos_ptr[0];  // first: the slicing waits for it
   const int s = blockIdx.x, g = blockIdx.y;
   const int grp = Hq / Hkv;
-  const int pos0 = pos_ptr[0];
-  const int Lmax = min(pos0 + n, max_len);  // attended length of the last row
-  const int beg = s * CH;
-  const bool attend = beg < Lmax;  // slice holds an attended position (uniform per workgroup)
-  if (!attend && !(FUSED && s == 0)) return;  // (slice 0 of the fused kernel still writes q_out)
-  const int end = max(min(beg + CH, Lmax), beg);
-
   const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
   const int c = lane & 15, g4 = lane >> 4;
   const int ncols = grp * n;
 
+  // Q^T as the MFMA B operand. Column ct*16+c is (row t, head g*grp+j), col = t*grp + j.
+  // Lane group g4 holds dims [32ks + 8g4, +8) of k-step ks (the same dims as the K operand).
+  // Loaded before pos arrives (it does not depend on it); the fused kernel preps it further down.
+  bf16x8_t qb[NT][8];
+  int trow[NT];  // the column's row (n for padding columns)
+#pragma unroll
+  for (int ct = 0; ct < NT; ++ct) {
+    const int col = ct * 16 + c;
+    const int t = col / grp, j = col - t * grp;
+    trow[ct] = col < ncols ? t : n;
+    if (!FUSED && col < ncols) {
+      const u32x4_t* src =
+          reinterpret_cast<const u32x4_t*>(q + (size_t)t * Hq * HD + (size_t)(g * grp + j) * HD);
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) qb[ct][ks] = as_bf16x8(src[4 * ks + g4]);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) qb[ct][ks] = as_bf16x8(u32x4_t{0u, 0u, 0u, 0u});
+    }
+  }
+
+  int ch0, tB;
+  call_split(pos0, n, max_len, NS, nd, ch0, tB);
+  if constexpr (!MULTI) tB = 1;  // one row: one pass
+  const int npass = tB < n ? 2 : 1;
+  const Pass PA = pass_of(0, ch0, tB, n, pos0, max_len, s);
+  const Pass PB = pass_of(1, ch0, tB, n, pos0, max_len, s);
+  const bool attendA = PA.beg < PA.end, attendB = MULTI && npass > 1 && PB.beg < PB.end;
+  const bool attend = attendA || attendB;  // uniform per workgroup
+  if (!attend && !(FUSED && s == 0)) return;  // (slice 0 of the fused kernel still writes q_out)
+
   __shared__ __attribute__((aligned(16))) char lds[lds_k_bytes<WAVES>()];
   __shared__ float s_m[WAVES][16 * NT], s_l[WAVES][16 * NT];
   u32x4_t* ks_lds = reinterpret_cast<u32x4_t*>(lds) + w * TILE * ROW_CHUNKS;
-
-  const int Lmin = min(pos0 + 1, max_len);  // row 0 attends the fewest positions
   const size_t head_off = (size_t)g * max_len * HD;
-  const uint32_t bytes = (uint32_t)max(end, 0) * (uint32_t)(HD * 2);  // loads past the slice read 0
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kc + head_off, bytes);
-  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vc + head_off, bytes);
 
-  int p0 = beg + w * TILE;  // this wave's first tile
-  VTile buf;
-  bool issued = false;
   if constexpr (FUSED) {
-    // rows t in [t_lo, t_hi) sit at positions in this slice: their K/V rows are written here
-    const int t_lo = max(beg - pos0, 0);
-    const int t_hi = attend ? max(min(end - pos0, n), t_lo) : t_lo;  // empty when none is here
+    // rows t in [t_lo, t_hi) sit at positions this workgroup reads: their K/V rows are written here
+    const int lo = attendA ? PA.beg : PB.beg, hi = attendB ? PB.end : PA.end;
+    const int t_lo = max(lo - pos0, 0);
+    const int t_hi = attend ? max(min(hi - pos0, n), t_lo) : t_lo;  // empty when none is here
     PrepRegs<NT> pr;
     fused_prep_load<NT>(pr, pin, g, grp, n, ncols, t_lo, t_hi);
     fused_prep_compute<NT>(pr, pin, s, g, grp, n, Hq, ncols, pos0, t_lo, t_hi, max_len,
                            const_cast<__bf16*>(kc), const_cast<__bf16*>(vc),
                            std::make_integer_sequence<int, PrepShape<NT>::MAXI>{});
     if (!attend) return;  // slice 0 beyond every attended position: q_out written, nothing else
-  }
-
-  // Q^T as the MFMA B operand. Column ct*16+c is (row t, head g*grp+j), col = t*grp + j.
-  // Lane group g4 holds dims [32ks + 8g4, +8) of k-step ks (the same dims as the K operand).
-  bf16x8_t qb[NT][8];
-  int Lcol[NT];
-#pragma unroll
-  for (int ct = 0; ct < NT; ++ct) {
-    const int col = ct * 16 + c;
-    if (col < ncols) {
-      const int t = col / grp, j = col - t * grp;
-      Lcol[ct] = min(pos0 + t + 1, max_len);
-      if constexpr (FUSED) {
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) qb[ct][ks] = as_bf16x8(fused_q_lds(col, 4 * ks + g4));
-      } else {
-        const u32x4_t* src =
-            reinterpret_cast<const u32x4_t*>(q + (size_t)t * Hq * HD + (size_t)(g * grp + j) * HD);
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) qb[ct][ks] = as_bf16x8(src[4 * ks + g4]);
-      }
-    } else {
-      Lcol[ct] = 0;  // padding column: every position masked
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) qb[ct][ks] = as_bf16x8(u32x4_t{0u, 0u, 0u, 0u});
-    }
-  }
-
-  float m[NT], l[NT];
-  f32x4_t acc[NT][16];  // [8hh + i]: O^T dims 128hh + 32g4 + 8ii + i (tile::pv_half)
-#pragma unroll
-  for (int ct = 0; ct < NT; ++ct) {
-    m[ct] = -INFINITY;
-    l[ct] = 0.f;
-#pragma unroll
-    for (int a = 0; a < 16; ++a) acc[ct][a] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  }
-
-  for (; p0 < end; p0 += WAVES * TILE) {
-    if (!issued) load_tile(buf, ks_lds, krs, vrs, p0, lane, c, g4);
-    issued = false;
-    wait_and_compute<NT>(buf, ks_lds, p0, Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
-  }
-
-  // ---- merge the waves of this workgroup in a fixed order and write the slice's partial
-#pragma unroll
-  for (int ct = 0; ct < NT; ++ct) l[ct] = group4_sum(l[ct]);
-
-  if (g4 == 0) {
 #pragma unroll
     for (int ct = 0; ct < NT; ++ct) {
-      s_m[w][ct * 16 + c] = m[ct];
-      s_l[w][ct * 16 + c] = l[ct];
-    }
-  }
-  __syncthreads();  // also: every wave is done with its K tile, so `lds` can hold the merge
-
-  float wsc[NT][WAVES];
+      const int col = ct * 16 + c;
+      if (col < ncols) {
 #pragma unroll
-  for (int ct = 0; ct < NT; ++ct) {
-    const int col = ct * 16 + c;
-    float M = -INFINITY;
-#pragma unroll
-    for (int v = 0; v < WAVES; ++v) M = fmaxf(M, s_m[v][col]);
-    float L = 0.f;
-#pragma unroll
-    for (int v = 0; v < WAVES; ++v) {
-      const float mv = s_m[v][col];
-      wsc[ct][v] = mv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv - M);
-      L += s_l[v][col] * wsc[ct][v];
-    }
-    if (w == 0 && g4 == 0 && col < ncols) {
-      const int t = col / grp, head = g * grp + (col - t * grp);
-      float* ml = part_ml + (((size_t)t * Hq + head) * NS + s) * 2;
-      ml[0] = M;
-      ml[1] = L;
-    }
-  }
-
-  // Each wave parks the O^T accumulators of its real columns in LDS as 16-byte rows (lanes of
-  // padding columns stay idle, which keeps the LDS traffic to what the merge needs), one barrier,
-  // then thread (w, lane) merges h = w/2, i in [4(w&1), +4) over waves 0..3 in that order and
-  // writes 4 x 16 bytes: dims 128h + 32g4 + 8ii + 4(w&1) + [0, 4) for ii = 0..3.
-  static_assert(WAVES == 4, "merge layout assumes 4 waves");
-  static_assert(WAVES * 16 * WAVE * 16 <= lds_k_bytes<WAVES>(), "merge buffer aliases the K tiles");
-  f32x4_t (*s_acc)[16][WAVE] = reinterpret_cast<f32x4_t (*)[16][WAVE]>(lds);
-#pragma unroll
-  for (int ct = 0; ct < NT; ++ct) {
-    const int col = ct * 16 + c;
-    if (ct > 0) __syncthreads();  // the previous column tile's reads are done
-    if (col < ncols) {
-#pragma unroll
-      for (int a = 0; a < 16; ++a) s_acc[w][a][lane] = acc[ct][a];
-    }
-    __syncthreads();
-    if (col < ncols) {
-      const int h = w >> 1, i0 = 4 * (w & 1);
-      f32x4_t mo[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        f32x4_t sum = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int v = 0; v < WAVES; ++v) sum += s_acc[v][8 * h + i0 + k][lane] * wsc[ct][v];
-        mo[k] = sum;
+        for (int ks = 0; ks < 8; ++ks) qb[ct][ks] = as_bf16x8(fused_q_lds(col, 4 * ks + g4));
       }
-      const int t = col / grp, head = g * grp + (col - t * grp);
-      float* dst = part_o + (((size_t)t * Hq + head) * NS + s) * HD + 128 * h + 32 * g4 + i0;
+    }
+  }
+
+  // One pass, inlined once per call of the lambda (as a loop over passes, the merge's
+  // loop-invariant addresses would be hoisted and stay live through the tile loop).
+  auto run_pass = [&](const Pass P) __attribute__((always_inline)) {
+    int Lcol[NT];  // attended length of the pass's columns; 0 (all masked) for the others
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii)
-        reinterpret_cast<f32x4_t*>(dst + 8 * ii)[0] =
-            f32x4_t{mo[0][ii], mo[1][ii], mo[2][ii], mo[3][ii]};
+    for (int ct = 0; ct < NT; ++ct)
+      Lcol[ct] = in_pass(ct * 16 + c, grp, P) ? min(pos0 + trow[ct] + 1, max_len) : 0;
+    const uint32_t bytes = (uint32_t)P.end * (uint32_t)(HD * 2);  // loads past the slice read 0
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc_uniform(kc + head_off, bytes);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc_uniform(vc + head_off, bytes);
+
+    float m[NT], l[NT];
+    f32x4_t acc[NT][16];  // [8hh + i]: O^T dims 128hh + 32g4 + 8ii + i (tile::pv_half)
+#pragma unroll
+    for (int ct = 0; ct < NT; ++ct) {
+      m[ct] = -INFINITY;
+      l[ct] = 0.f;
+#pragma unroll
+      for (int a = 0; a < 16; ++a) acc[ct][a] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+
+    VTile buf;
+    for (int p0 = P.beg + w * TILE; p0 < P.end; p0 += WAVES * TILE) {
+      load_tile(buf, ks_lds, krs, vrs, p0, lane, c, g4);
+      wait_and_compute<NT>(buf, ks_lds, p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
+    }
+
+    // ---- merge the waves of this workgroup in a fixed order and write the slice's partial
+#pragma unroll
+    for (int ct = 0; ct < NT; ++ct) l[ct] = group4_sum(l[ct]);
+
+    if (g4 == 0) {
+#pragma unroll
+      for (int ct = 0; ct < NT; ++ct) {
+        s_m[w][ct * 16 + c] = m[ct];
+        s_l[w][ct * 16 + c] = l[ct];
+      }
+    }
+    __syncthreads();  // also: every wave is done with its K tile, so `lds` can hold the merge
+
+    float wsc[NT][WAVES];
+#pragma unroll
+    for (int ct = 0; ct < NT; ++ct) {
+      const int col = ct * 16 + c;
+      float M = -INFINITY;
+#pragma unroll
+      for (int v = 0; v < WAVES; ++v) M = fmaxf(M, s_m[v][col]);
+      float L = 0.f;
+#pragma unroll
+      for (int v = 0; v < WAVES; ++v) {
+        const float mv = s_m[v][col];
+        wsc[ct][v] = mv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv - M);
+        L += s_l[v][col] * wsc[ct][v];
+      }
+      if (w == 0 && g4 == 0 && in_pass(col, grp, P)) {
+        const int t = trow[ct], head = g * grp + (col - t * grp);
+        float* ml = part_ml + (((size_t)t * Hq + head) * NS + s) * 2;
+        ml[0] = M;
+        ml[1] = L;
+      }
+    }
+
+    // Each wave parks the O^T accumulators of the pass's columns in LDS as 16-byte rows (lanes of
+    // other columns stay idle, which keeps the LDS traffic to what the merge needs), one barrier,
+    // then thread (w, lane) merges h = w/2, i in [4(w&1), +4) over waves 0..3 in that order and
+    // writes 4 x 16 bytes: dims 128h + 32g4 + 8ii + 4(w&1) + [0, 4) for ii = 0..3.
+    static_assert(WAVES == 4, "merge layout assumes 4 waves");
+    static_assert(WAVES * 16 * WAVE * 16 <= lds_k_bytes<WAVES>(), "merge buffer aliases the K tiles");
+    f32x4_t (*s_acc)[16][WAVE] = reinterpret_cast<f32x4_t (*)[16][WAVE]>(lds);
+#pragma unroll
+    for (int ct = 0; ct < NT; ++ct) {
+      const int col = ct * 16 + c;
+      const bool mine = in_pass(col, grp, P);
+      if (ct > 0) __syncthreads();  // the previous column tile's reads are done
+      if (mine) {
+#pragma unroll
+        for (int a = 0; a < 16; ++a) s_acc[w][a][lane] = acc[ct][a];
+      }
+      __syncthreads();
+      if (mine) {
+        const int h = w >> 1, i0 = 4 * (w & 1);
+        f32x4_t mo[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          f32x4_t sum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int v = 0; v < WAVES; ++v) sum += s_acc[v][8 * h + i0 + k][lane] * wsc[ct][v];
+          mo[k] = sum;
+        }
+        const int t = trow[ct], head = g * grp + (col - t * grp);
+        float* dst = part_o + (((size_t)t * Hq + head) * NS + s) * HD + 128 * h + 32 * g4 + i0;
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii)
+          reinterpret_cast<f32x4_t*>(dst + 8 * ii)[0] =
+              f32x4_t{mo[0][ii], mo[1][ii], mo[2][ii], mo[3][ii]};
+      }
+    }
+  };
+  if (attendA) run_pass(PA);
+  if constexpr (MULTI) {
+    if (attendB) {
+      if (attendA) __syncthreads();  // the merge's LDS reads are done before the next pass
+      run_pass(PB);
     }
   }
 }
@@ -476,165 +564,176 @@ __global__ void __launch_bounds__(cols::SUBSETS * (NT / CPW) * WAVE)
 attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
                           const __bf16* __restrict__ vc, const int* __restrict__ pos_ptr,
                           float* __restrict__ part_o, float* __restrict__ part_ml, int n, int Hq,
-                          int Hkv, int max_len, int NS, int CH, float scale_log2) {
+                          int Hkv, int max_len, int NS, NsDiv nd, float scale_log2) {
   static_assert(NT % CPW == 0, "column tiles split evenly over the waves of a subset");
   constexpr int SUB = cols::SUBSETS;
   constexpr int WPS = NT / CPW;  // waves per subset
+  const int pos0 = pos_ptr[0];  // first: the slicing waits for it
   const int s = blockIdx.x, g = blockIdx.y;
   const int grp = Hq / Hkv;
-  const int pos0 = pos_ptr[0];
-  const int Lmax = min(pos0 + n, max_len);
-  const int beg = s * CH;
-  if (beg >= Lmax) return;  // uniform per workgroup
-  const int end = min(beg + CH, Lmax);
-
   const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
   const int sub = w % SUB, rank = w / SUB;
   const int c = lane & 15, g4 = lane >> 4;
   const int ncols = grp * n;
 
-  __shared__ __attribute__((aligned(16))) u32x4_t lds[SUB * cols::REGION_U4];  // 128 KB
-  __shared__ float s_m[SUB][16 * NT], s_l[SUB][16 * NT];
-
-  bf16x8_t qb[CPW][8];
-  int Lcol[CPW];
+  bf16x8_t qb[CPW][8];  // loaded before pos arrives (it does not depend on it)
 #pragma unroll
   for (int u = 0; u < CPW; ++u) {
     const int col = (rank * CPW + u) * 16 + c;
     if (col < ncols) {
       const int t = col / grp, j = col - t * grp;
-      Lcol[u] = min(pos0 + t + 1, max_len);
       const u32x4_t* src =
           reinterpret_cast<const u32x4_t*>(q + (size_t)t * Hq * HD + (size_t)(g * grp + j) * HD);
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) qb[u][ks] = as_bf16x8(src[4 * ks + g4]);
     } else {
-      Lcol[u] = 0;
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) qb[u][ks] = as_bf16x8(u32x4_t{0u, 0u, 0u, 0u});
     }
   }
 
-  const int Lmin = min(pos0 + 1, max_len);
+  int ch0, tB;
+  call_split(pos0, n, max_len, NS, nd, ch0, tB);
+  const int npass = tB < n ? 2 : 1;
+  const Pass PA = pass_of(0, ch0, tB, n, pos0, max_len, s);
+  const Pass PB = pass_of(1, ch0, tB, n, pos0, max_len, s);
+  const bool attendA = PA.beg < PA.end;
+  if (!attendA && !(npass > 1 && PB.beg < PB.end)) return;  // uniform per workgroup
+
+  __shared__ __attribute__((aligned(16))) u32x4_t lds[SUB * cols::REGION_U4];  // 128 KB
+  __shared__ float s_m[SUB][16 * NT], s_l[SUB][16 * NT];
   const size_t head_off = (size_t)g * max_len * HD;
-  const uint32_t bytes = (uint32_t)end * (uint32_t)(HD * 2);
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kc + head_off, bytes);
-  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vc + head_off, bytes);
-
-  float m[CPW], l[CPW];
-  f32x4_t acc[CPW][16];
-#pragma unroll
-  for (int u = 0; u < CPW; ++u) {
-    m[u] = -INFINITY;
-    l[u] = 0.f;
-#pragma unroll
-    for (int a = 0; a < 16; ++a) acc[u][a] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  }
-
   u32x4_t* kt = lds + sub * cols::REGION_U4;
   const u32x4_t* vt = kt + cols::TILE_U4;
-  const int ntiles = (end - beg + TILE - 1) / TILE;
-  const int rounds = (ntiles + SUB - 1) / SUB;
-  for (int r = 0; r < rounds; ++r) {
-    const int p0 = beg + (r * SUB + sub) * TILE;  // this subset's tile in round r
-    const bool has = p0 < end;                     // uniform per subset
-    if (has) {
-      // The subset's WPS waves share its 32 LDS-DMA loads: 16 of K (rows 2i, 2i+1, swizzled as
-      // k_slot) and 16 of V (row-major), one KB of contiguous cache each.
-      for (int i = rank; i < 32; i += WPS) {
-        const int j = i & 15, row = 2 * j + (lane >> 5);
-        if (i < 16)
-          buffer_load16_to_lds(krs, (uint32_t)(p0 + row) * (HD * 2) + ((lane & 31) ^ (row & 15)) * 16,
-                               kt + 2 * j * ROW_CHUNKS);
-        else
-          buffer_load16_to_lds(vrs, (uint32_t)(p0 + row) * (HD * 2) + (lane & 31) * 16,
-                               kt + cols::TILE_U4 + 2 * j * ROW_CHUNKS);
-      }
-    }
-    vmcnt_wait<0>();
-    __syncthreads();  // every wave's loads of this round have landed
-    if (has) {
-      f32x4_t sacc[CPW][2];
-      tile::qk_tile<CPW>(kt, qb, c, g4, sacc);
-      u32x4_t pb_hi[CPW], pb_lo[CPW];
-      if (p0 + TILE > Lmin)
-        tile::softmax_tile<CPW, true, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
-      else
-        tile::softmax_tile<CPW, false, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        u32x4_t vr[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          vr[e] = vt[(16 * (e >> 2) + 4 * g4 + (e & 3)) * ROW_CHUNKS + 16 * hh + c];
-        tile::pv_half<CPW, true>(vr, hh, pb_hi, pb_lo, acc);
-      }
-    }
-    __syncthreads();  // this round's tiles are read before the next round overwrites them
-  }
 
-  // ---- merge the 4 subsets in order 0..3 (as attn_partials_kernel merges its waves)
+  // One pass, inlined once per call of the lambda (a loop over passes would keep the merge's
+  // loop-invariant addresses live through the tile rounds and spill).
+  auto run_pass = [&](const Pass P) __attribute__((always_inline)) {
+    int Lcol[CPW];
 #pragma unroll
-  for (int u = 0; u < CPW; ++u) {
-    l[u] = group4_sum(l[u]);
-    if (g4 == 0) {
-      s_m[sub][(rank * CPW + u) * 16 + c] = m[u];
-      s_l[sub][(rank * CPW + u) * 16 + c] = l[u];
-    }
-  }
-  __syncthreads();
-  float wsc[CPW][SUB];
-#pragma unroll
-  for (int u = 0; u < CPW; ++u) {
-    const int col = (rank * CPW + u) * 16 + c;
-    float M = -INFINITY;
-#pragma unroll
-    for (int v = 0; v < SUB; ++v) M = fmaxf(M, s_m[v][col]);
-    float L = 0.f;
-#pragma unroll
-    for (int v = 0; v < SUB; ++v) {
-      const float mv = s_m[v][col];
-      wsc[u][v] = mv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv - M);
-      L += s_l[v][col] * wsc[u][v];
-    }
-    if (sub == 0 && g4 == 0 && col < ncols) {
-      const int t = col / grp, head = g * grp + (col - t * grp);
-      float* ml = part_ml + (((size_t)t * Hq + head) * NS + s) * 2;
-      ml[0] = M;
-      ml[1] = L;
-    }
-  }
-  f32x4_t (*s_acc)[16][WAVE] = reinterpret_cast<f32x4_t (*)[16][WAVE]>(lds);
-  static_assert(SUB * 16 * WAVE * 16 <= SUB * cols::REGION_U4 * 16, "merge buffer fits the ring");
-  for (int rr = 0; rr < WPS; ++rr) {
+    for (int u = 0; u < CPW; ++u)
+      Lcol[u] = in_pass((rank * CPW + u) * 16 + c, grp, P)
+                    ? min(pos0 + ((rank * CPW + u) * 16 + c) / grp + 1, max_len) : 0;
+    const uint32_t bytes = (uint32_t)P.end * (uint32_t)(HD * 2);
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc_uniform(kc + head_off, bytes);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc_uniform(vc + head_off, bytes);
+
+    float m[CPW], l[CPW];
+    f32x4_t acc[CPW][16];
 #pragma unroll
     for (int u = 0; u < CPW; ++u) {
-      const int col = (rr * CPW + u) * 16 + c;
-      if (rank == rr && col < ncols) {
+      m[u] = -INFINITY;
+      l[u] = 0.f;
 #pragma unroll
-        for (int a = 0; a < 16; ++a) s_acc[sub][a][lane] = acc[u][a];
-      }
-      __syncthreads();
-      if (rank == rr && col < ncols) {
-        const int h = sub >> 1, i0 = 4 * (sub & 1);
-        f32x4_t mo[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          f32x4_t sum = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int v = 0; v < SUB; ++v) sum += s_acc[v][8 * h + i0 + k][lane] * wsc[u][v];
-          mo[k] = sum;
-        }
-        const int t = col / grp, head = g * grp + (col - t * grp);
-        float* dst = part_o + (((size_t)t * Hq + head) * NS + s) * HD + 128 * h + 32 * g4 + i0;
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii)
-          reinterpret_cast<f32x4_t*>(dst + 8 * ii)[0] =
-              f32x4_t{mo[0][ii], mo[1][ii], mo[2][ii], mo[3][ii]};
-      }
-      __syncthreads();
+      for (int a = 0; a < 16; ++a) acc[u][a] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
-  }
+
+    const int ntiles = (P.end - P.beg + TILE - 1) / TILE;
+    const int rounds = (ntiles + SUB - 1) / SUB;
+    for (int r = 0; r < rounds; ++r) {
+      const int p0 = P.beg + (r * SUB + sub) * TILE;  // this subset's tile in round r
+      const bool has = p0 < P.end;                     // uniform per subset
+      if (has) {
+        // The subset's WPS waves share its 32 LDS-DMA loads: 16 of K (rows 2i, 2i+1, swizzled as
+        // k_slot) and 16 of V (row-major), one KB of contiguous cache each.
+        for (int i = rank; i < 32; i += WPS) {
+          const int j = i & 15, row = 2 * j + (lane >> 5);
+          if (i < 16)
+            buffer_load16_to_lds(krs, (uint32_t)(p0 + row) * (HD * 2) + ((lane & 31) ^ (row & 15)) * 16,
+                                 kt + 2 * j * ROW_CHUNKS);
+          else
+            buffer_load16_to_lds(vrs, (uint32_t)(p0 + row) * (HD * 2) + (lane & 31) * 16,
+                                 kt + cols::TILE_U4 + 2 * j * ROW_CHUNKS);
+        }
+      }
+      vmcnt_wait<0>();
+      __syncthreads();  // every wave's loads of this round have landed
+      if (has) {
+        f32x4_t sacc[CPW][2];
+        tile::qk_tile<CPW>(kt, qb, c, g4, sacc);
+        u32x4_t pb_hi[CPW], pb_lo[CPW];
+        if (p0 + TILE > P.Lmin)
+          tile::softmax_tile<CPW, true, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
+        else
+          tile::softmax_tile<CPW, false, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          u32x4_t vr[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            vr[e] = vt[(16 * (e >> 2) + 4 * g4 + (e & 3)) * ROW_CHUNKS + 16 * hh + c];
+          tile::pv_half<CPW, true>(vr, hh, pb_hi, pb_lo, acc);
+        }
+      }
+      __syncthreads();  // this round's tiles are read before the next round overwrites them
+    }
+
+    // ---- merge the 4 subsets in order 0..3 (as attn_partials_kernel merges its waves)
+#pragma unroll
+    for (int u = 0; u < CPW; ++u) {
+      l[u] = group4_sum(l[u]);
+      if (g4 == 0) {
+        s_m[sub][(rank * CPW + u) * 16 + c] = m[u];
+        s_l[sub][(rank * CPW + u) * 16 + c] = l[u];
+      }
+    }
+    __syncthreads();
+    float wsc[CPW][SUB];
+#pragma unroll
+    for (int u = 0; u < CPW; ++u) {
+      const int col = (rank * CPW + u) * 16 + c;
+      float M = -INFINITY;
+#pragma unroll
+      for (int v = 0; v < SUB; ++v) M = fmaxf(M, s_m[v][col]);
+      float L = 0.f;
+#pragma unroll
+      for (int v = 0; v < SUB; ++v) {
+        const float mv = s_m[v][col];
+        wsc[u][v] = mv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv - M);
+        L += s_l[v][col] * wsc[u][v];
+      }
+      if (sub == 0 && g4 == 0 && in_pass(col, grp, P)) {
+        const int t = col / grp, head = g * grp + (col - t * grp);
+        float* ml = part_ml + (((size_t)t * Hq + head) * NS + s) * 2;
+        ml[0] = M;
+        ml[1] = L;
+      }
+    }
+    f32x4_t (*s_acc)[16][WAVE] = reinterpret_cast<f32x4_t (*)[16][WAVE]>(lds);
+    static_assert(SUB * 16 * WAVE * 16 <= SUB * cols::REGION_U4 * 16, "merge buffer fits the ring");
+    for (int rr = 0; rr < WPS; ++rr) {
+#pragma unroll
+      for (int u = 0; u < CPW; ++u) {
+        const int col = (rr * CPW + u) * 16 + c;
+        const bool mine = rank == rr && in_pass(col, grp, P);
+        if (mine) {
+#pragma unroll
+          for (int a = 0; a < 16; ++a) s_acc[sub][a][lane] = acc[u][a];
+        }
+        __syncthreads();
+        if (mine) {
+          const int h = sub >> 1, i0 = 4 * (sub & 1);
+          f32x4_t mo[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            f32x4_t sum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int v = 0; v < SUB; ++v) sum += s_acc[v][8 * h + i0 + k][lane] * wsc[u][v];
+            mo[k] = sum;
+          }
+          const int t = col / grp, head = g * grp + (col - t * grp);
+          float* dst = part_o + (((size_t)t * Hq + head) * NS + s) * HD + 128 * h + 32 * g4 + i0;
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii)
+            reinterpret_cast<f32x4_t*>(dst + 8 * ii)[0] =
+                f32x4_t{mo[0][ii], mo[1][ii], mo[2][ii], mo[3][ii]};
+        }
+        __syncthreads();  // (also ends the pass: the next pass's loads may overwrite `lds`)
+      }
+    }
+  };
+  if (attendA) run_pass(PA);
+  if (npass > 1 && PB.beg < PB.end) run_pass(PB);
 }
 
 // Log-sum-exp merge of the slices holding row t's positions + fused sigmoid output gate.
@@ -649,7 +748,8 @@ constexpr int COMBINE_BATCH = 16;
 __global__ void __launch_bounds__(WAVE)
 attn_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml,
                     const int* __restrict__ pos_ptr, const __bf16* __restrict__ qg, long ldp,
-                    __bf16* __restrict__ out, long ldo, int Hq, int max_len, int NS, int CH) {
+                    __bf16* __restrict__ out, long ldo, int Hq, int max_len, int NS,
+                    NsDiv nd) {
   const int h = blockIdx.x, t = blockIdx.y, z = blockIdx.z;
   const int lane = threadIdx.x, c16 = lane & 15, sg = lane >> 4;
   const size_t base = ((size_t)t * Hq + h) * NS;
@@ -677,15 +777,18 @@ attn_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ 
 #pragma unroll
   for (int i = 0; i < 4; ++i) gate[i] = bf16_to_f32(gp[i]);
   const int L_t = min(pos_ptr[0] + t + 1, max_len);
-  const int S = L_t > 0 ? (L_t + CH - 1) / CH : 0;
+  const int CH = split_size(L_t, nd);  // slice s holds positions iff s * CH < L_t (s < NS)
 
   f32x4_t O = {0.f, 0.f, 0.f, 0.f};
   float L = 0.f, M = -INFINITY;
-  for (int s0 = 0; s0 < S; s0 += 4 * COMBINE_BATCH) {
-    if (s0 > 0) load_batch(s0, S);
+  for (int s0 = 0; s0 < NS && s0 * CH < L_t; s0 += 4 * COMBINE_BATCH) {
+    if (s0 > 0) load_batch(s0, NS);
     bool valid[COMBINE_BATCH];
 #pragma unroll
-    for (int b = 0; b < COMBINE_BATCH; ++b) valid[b] = s0 + 4 * b + sg < S;
+    for (int b = 0; b < COMBINE_BATCH; ++b) {
+      const int sl = s0 + 4 * b + sg;
+      valid[b] = sl < NS && sl * CH < L_t;
+    }
     // running max over all slices seen so far (every lane group, so M is wave-uniform)
     float bm = M;
 #pragma unroll
@@ -734,9 +837,8 @@ static hipError_t check_decode_shape(int n, int Hq, int Hkv, int max_len, int NS
 static hipError_t launch_partials(const void* q, const void* kc, const void* vc, const int* pos,
                                   float* part_o, float* part_ml, int n, int Hq, int Hkv,
                                   int max_len, int NS, float scale, hipStream_t stream) {
-  const int CH = split_size(max_len, NS);
-  const int slices = (max_len + CH - 1) / CH;  // <= NS; later slices never hold positions
-  const dim3 grid(slices, Hkv);
+  const dim3 grid(max_slices(max_len, NS), Hkv);
+  const NsDiv nd = ns_div(NS);
   const float scale_log2 = scale * 1.4426950408889634f;
   const int NT = ((Hq / Hkv) * n + 15) / 16;
   const auto* Q = static_cast<const __bf16*>(q);
@@ -745,10 +847,15 @@ static hipError_t launch_partials(const void* q, const void* kc, const void* vc,
   // NT = 1, 2: every wave holds all column tiles (measured fastest at 1-5 rows, GQA 6).
   // NT = 3, 4: one subset wave per column tile (the one-tile kernel would spill: 2.3-2.8x slower).
   switch (NT) {
-    case 1: attn_partials_kernel<1><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2, PrepIn{}); break;
-    case 2: attn_partials_kernel<2><<<grid, dim3(waves_for<2>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2, PrepIn{}); break;
-    case 3: attn_partials_cols_kernel<3, 1><<<grid, dim3(cols::SUBSETS * 3 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
-    default: attn_partials_cols_kernel<4, 2><<<grid, dim3(cols::SUBSETS * 2 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2); break;
+    case 1:
+      if (n == 1)
+        attn_partials_kernel<1, false, false><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{});
+      else
+        attn_partials_kernel<1><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{});
+      break;
+    case 2: attn_partials_kernel<2><<<grid, dim3(waves_for<2>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{}); break;
+    case 3: attn_partials_cols_kernel<3, 1><<<grid, dim3(cols::SUBSETS * 3 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2); break;
+    default: attn_partials_cols_kernel<4, 2><<<grid, dim3(cols::SUBSETS * 2 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2); break;
   }
   return hipGetLastError();
 }
@@ -756,10 +863,9 @@ static hipError_t launch_partials(const void* q, const void* kc, const void* vc,
 static hipError_t launch_combine(const float* part_o, const float* part_ml, const int* pos,
                                  const void* qg, long ldp, void* out, long ldo, int n, int Hq,
                                  int max_len, int NS, hipStream_t stream) {
-  const int CH = split_size(max_len, NS);
   attn_combine_kernel<<<dim3(Hq, n, HD / COMBINE_DIMS), dim3(WAVE), 0, stream>>>(
       part_o, part_ml, pos, static_cast<const __bf16*>(qg), ldp, static_cast<__bf16*>(out), ldo,
-      Hq, max_len, NS, CH);
+      Hq, max_len, NS, ns_div(NS));
   return hipGetLastError();
 }
 
@@ -767,9 +873,9 @@ static hipError_t launch_combine(const float* part_o, const float* part_ml, cons
 
 using namespace qe;
 
-extern "C" int qe_attn_split_size(int max_len, int NS) {
-  if (max_len < 1 || NS < 1) return 0;
-  return split_size(max_len, NS);
+extern "C" int qe_attn_split_size(int L, int NS) {
+  if (L < 1 || NS < 1 || L >= SPLIT_L_MAX) return 0;
+  return split_size(L, ns_div(NS));  // the kernels' own arithmetic
 }
 
 extern "C" hipError_t qe_attn_decode_partials(const void* q, const void* kc, const void* vc,
@@ -834,8 +940,8 @@ extern "C" hipError_t qe_attn_prep_decode(const void* qg, const void* k, const v
     return qe_attn_decode(q_out, kc, vc, pos, qg, ldp, part_o, part_ml, out, ldo, n, Hq, Hkv,
                           max_len, NS, scale, stream);
   }
-  const int CH = split_size(max_len, NS);
-  const dim3 grid((max_len + CH - 1) / CH, Hkv);
+  const dim3 grid(max_slices(max_len, NS), Hkv);
+  const NsDiv nd = ns_div(NS);
   const PrepIn pin{static_cast<const __bf16*>(qg), static_cast<const __bf16*>(k),
                    static_cast<const __bf16*>(v), ldp, static_cast<const __bf16*>(qnw),
                    static_cast<const __bf16*>(knw), inv_freq, static_cast<__bf16*>(q_out), rd,
@@ -843,12 +949,15 @@ extern "C" hipError_t qe_attn_prep_decode(const void* qg, const void* k, const v
   const float scale_log2 = scale * 1.4426950408889634f;
   const auto* K = static_cast<const __bf16*>(kc);
   const auto* V = static_cast<const __bf16*>(vc);
-  if (NT == 1)
+  if (NT == 1 && n == 1)
+    attn_partials_kernel<1, true, false><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(
+        nullptr, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, pin);
+  else if (NT == 1)
     attn_partials_kernel<1, true><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(
-        nullptr, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2, pin);
+        nullptr, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, pin);
   else
     attn_partials_kernel<2, true><<<grid, dim3(waves_for<2>() * WAVE), 0, stream>>>(
-        nullptr, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, CH, scale_log2, pin);
+        nullptr, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, pin);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   return qe_attn_decode_combine(part_o, part_ml, pos, qg, ldp, out, ldo, n, Hq, max_len, NS,

@@ -150,6 +150,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
 }
+// The same for a base and size that are wave-uniform where the compiler cannot prove it (values
+// merged across branches): readfirstlane keeps the resource in SGPRs, since a resource in VGPRs
+// turns every buffer load into a waterfall loop.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_uniform(const void* base,
+                                                                    uint32_t bytes) {
+  // readfirstlane returns int: go through uint32_t so the low half is zero-extended, not
+  // sign-extended into the high half.
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+  return make_rsrc(reinterpret_cast<const void*>(((uint64_t)hi << 32) | (uint64_t)lo),
+                   (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes));
+}
 __device__ __forceinline__ u32x4_t buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   return __builtin_bit_cast(u32x4_t,
                             __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0));

@@ -183,7 +183,7 @@ def test_config3_mtp_verify(native):
 # ------------------------------------------------------------------ semantics and edge cases
 @pytest.mark.parametrize("ns", [1, 3, 16, 100, 1000])
 def test_split_count_does_not_matter(native, ns):
-    """Any split count gives the oracle's answer (slices of split_size(max_len, NS) positions)."""
+    """Any split count gives the oracle's answer (row t in slices of split_size(L_t, NS))."""
     case = decode_case(seed=7, hq=24, hkv=4, pos=3000, n=3, max_len=5000)
     ok, mx, mean = attn_close(gpu_decode(native, case, ns), oracle_decode(case))
     assert ok, (ns, mx, mean)
@@ -199,6 +199,40 @@ def test_gqa_shapes_and_rows(native, hq, hkv, n):
     assert ok, (mx, mean)
     for t in range(n):
         o1 = gpu_decode(native, case, 8, pos=case.pos + t, rows=slice(t, t + 1))
+        assert torch.equal(o1[0], out[t]), t
+
+
+@pytest.mark.parametrize("hq,hkv,n,pos,ns", [
+    (24, 4, 2, 2047, 64),   # lengths 2048 | 2049: slices of 32 | 64 (one column tile)
+    (24, 4, 5, 2046, 64),   # 2 + 3 rows (two column tiles)
+    (24, 4, 8, 2044, 64),   # 4 + 4 rows (three column tiles, one wave per tile)
+    (32, 4, 8, 2044, 64),   # four column tiles
+    (24, 4, 8, 4092, 64),   # slices of 64 | 96
+    (8, 2, 4, 510, 16),     # 2 + 2 rows, 16 splits
+    (8, 2, 3, 30, 1),       # one split: slices of 32 | 64
+])
+def test_rows_straddling_a_slice_size_change(native, hq, hkv, n, pos, ns):
+    """The rows of one call fall on both sides of a change of slice size (the call runs one pass
+    per size): results match the oracle and each row is bit-identical to a 1-row call."""
+    case = decode_case(seed=pos + n, hq=hq, hkv=hkv, pos=pos, n=n, max_len=pos + n + 40)
+    out = gpu_decode(native, case, ns)
+    ok, mx, mean = attn_close(out, oracle_decode(case))
+    assert ok, (mx, mean)
+    for t in range(n):
+        o1 = gpu_decode(native, case, ns, pos=case.pos + t, rows=slice(t, t + 1))
+        assert torch.equal(o1[0], out[t]), t
+
+
+@pytest.mark.parametrize("n,pos", [(1, 1000), (5, 3000), (8, 200)])
+def test_short_prefix_in_a_long_cache(native, n, pos):
+    """A cache far longer than the attended prefix: slices follow the attended length (the
+    reference's ceil(L/NS), attn.cu:78-80), results match the oracle and rows stay bit-exact."""
+    case = decode_case(seed=n * 7 + pos, hq=24, hkv=4, pos=pos, n=n, max_len=32768)
+    out = gpu_decode(native, case, 64)
+    ok, mx, mean = attn_close(out, oracle_decode(case))
+    assert ok, (mx, mean)
+    for t in range(n):
+        o1 = gpu_decode(native, case, 64, pos=case.pos + t, rows=slice(t, t + 1))
         assert torch.equal(o1[0], out[t]), t
 
 

@@ -2,6 +2,7 @@
 include/qe_attn.h declares, the C ABI rejects out-of-range arguments before launching anything,
 and the torch extension enforces the reference's validation contract
 (reference csrc/bindings.cpp:15-30,147-183). No kernel runs here."""
+import random
 import re
 from pathlib import Path
 
@@ -41,10 +42,27 @@ def test_version_and_split_size(capi):
     assert capi.split_size(1000, 3) == 352           # ceil(1000/3) = 334 -> multiple of 32
     assert capi.split_size(10, 100) == 32            # never below one 32-position tile
     assert capi.split_size(0, 4) == 0 and capi.split_size(8, 0) == 0
-    for max_len in (1, 31, 32, 33, 4097, 131072):
+    for L in (1, 31, 32, 33, 4097, 131072):    # slice size of a row attending L positions
         for ns in (1, 7, 16, 512):
-            ch = capi.split_size(max_len, ns)
-            assert ch % 32 == 0 and ch * ns >= max_len
+            ch = capi.split_size(L, ns)
+            assert ch % 32 == 0 and ch * ns >= L and (ch == 32 or ch - 32 < -(-L // ns))
+    assert capi.split_size(1 << 23, 4) == 0      # beyond the kernels' length range
+
+
+def test_split_size_multiply_shift_is_exact(capi):
+    """The kernels divide by NS with a host-computed multiply and shift; qe_attn_split_size runs
+    the same inline arithmetic. Compare it with exact integer division at the edges of the
+    length range, at multiples of NS and their neighbours, and at seeded random points."""
+    rng = random.Random(5)
+    ns_list = [1, 2, 3, 5, 7, 16, 31, 64, 100, 127, 128, 129, 1000, 4095, 65537, (1 << 23) - 1,
+               (1 << 31) - 1] + [rng.randrange(1, 1 << 20) for _ in range(40)]
+    top = (1 << 23) - 1
+    for ns in ns_list:
+        Ls = {1, 2, top, top - 1, ns, ns + 1, 2 * ns, 2 * ns + 1, 32 * ns, 32 * ns + 1}
+        Ls |= {rng.randrange(1, top + 1) for _ in range(60)}
+        for L in sorted(x for x in Ls if 1 <= x <= top):
+            want = max(32, -(-(-(-L // ns)) // 32) * 32)
+            assert capi.split_size(L, ns) == want, (L, ns)
 
 
 # Fake 16-byte aligned addresses: the C ABI validates before touching them.

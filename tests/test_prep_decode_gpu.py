@@ -52,6 +52,8 @@ def _run(C, fused, kc, vc, pr, qnw, knw, inv, pos, hq, ns):
     (6, 1, 4, 62, 64, 2),             # rows past the end of the cache are not written
     (4, 4, 1, 0, 16, 1),              # first position, no GQA
     (24, 4, 2, 131070, 131072, 64),   # long cache
+    (24, 4, 2, 2047, 4096, 64),       # rows straddle a slice-size change (32 | 64): two passes
+    (24, 4, 5, 2046, 2100, 64),       # the same with two column tiles
 ])
 def test_prep_decode_equals_prep_then_decode(native, hq, hkv, n, pos, max_len, ns):
     kc, vc, pr, qnw, knw, inv = _inputs(hq, hkv, n, pos, max_len, seed=hq * 100 + n)
