@@ -267,6 +267,45 @@ def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
     del kcs, vcs
 
     res.update(bench_prefill(torch, C, steps, warmup))
+    res.update(bench_gemv(torch, C, qa, steps, warmup))
+    return res
+
+
+def bench_gemv(torch, C, qa, steps: int, warmup: int) -> dict:
+    """The projections on either side of the attention path (F1's neighbours): in_proj
+    [14336 x 5120] and o_proj [5120 x 6144] GEMV at 1 and 5 rows, each call on a different copy
+    of the weights (>= 600 MB in rotation, past the 256 MB Infinity Cache); plus the streaming
+    read probe over 2 GiB, the achievable HBM read rate on the same box."""
+    import qengine_amd.capi as capi
+    dev, BF = "cuda", torch.bfloat16
+    gen = torch.Generator(device=dev).manual_seed(2)
+    res = {}
+    for name, N, K in (("gemv_in_proj_14336x5120", 14336, 5120),
+                       ("gemv_o_proj_5120x6144", 5120, 6144)):
+        wbytes = N * K * 2
+        copies = max(4, -(-600 * 2 ** 20 // wbytes))
+        Ws = [(torch.randn(N, K, device=dev, generator=gen) * K ** -0.5).to(BF)
+              for _ in range(copies)]
+        for nr in (1, 5):
+            x = torch.randn(nr, K, device=dev, generator=gen).to(BF)
+            out = torch.empty(nr, N, dtype=BF, device=dev)
+
+            def run():
+                for W in Ws:
+                    C.gemv_bf16(W, x, out)
+            us = time_fn_graph(torch, run, steps, warmup) * 1e3 / copies
+            gbps = wbytes / (us * 1e3)
+            res[f"{name}_rows{nr}"] = {"us": round(us, 3), "GBps": round(gbps, 1),
+                                       "hbm_frac": round(gbps / HBM_PEAK_GBS, 4),
+                                       "kparts": capi.gemv_kparts(N, K)}
+        del Ws
+    nbytes = 2 * 2 ** 30
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    us = time_fn_graph(torch, lambda: capi.hbm_read_probe(buf, nbytes, sink), steps, warmup) * 1e3
+    res["hbm_read_probe_2GiB"] = {"us": round(us, 2), "GBps": round(nbytes / (us * 1e3), 1),
+                                  "hbm_frac": round(nbytes / (us * 1e3) / HBM_PEAK_GBS, 4)}
+    del buf
     return res
 
 
@@ -357,6 +396,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only BASELINE config 5 (chunked prefill); prints its timing as JSON")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only the in_proj / o_proj GEMV and the HBM read probe, as JSON")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other BASELINE configs (1, 3, 4, 5)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -386,6 +427,9 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
     if args.prefill_only:
         print(json.dumps(bench_prefill(torch, C, args.steps, args.warmup)))
+        return
+    if args.gemv_only:
+        print(json.dumps(bench_gemv(torch, C, qa, args.steps, args.warmup)))
         return
     lengths = [int(x) for x in args.lengths.split(",") if x]
     if HEADLINE_L not in lengths:

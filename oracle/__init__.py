@@ -10,5 +10,8 @@ Parity status per function (each is pinned by checks in ``tests/test_oracle.py``
   attention_core, attention_core_grouped, attn_prep, attn_decode, attn_prefill,
   flash_decode_fp64                                   -> pinned (closed forms, brute force,
                                                          invariants, bf16 rounding model)
+  gemv_exact, gemv_bound, gemv_bf16_ref               -> pinned (brute-force loops, one-hot and
+                                                         identity closed forms, NaN, the bound)
 """
 from .attn_oracle import *  # noqa: F401,F403
+from .gemv_oracle import gemv_bf16_ref, gemv_bound, gemv_exact  # noqa: F401

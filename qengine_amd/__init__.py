@@ -28,6 +28,7 @@ from ._C import (  # noqa: E402,F401
     attn_prep,
     attn_prep_chunk,
     attn_prep_decode,
+    gemv_bf16,
     set_pdl_launch,
     set_pdl_trigger,
     split_size,

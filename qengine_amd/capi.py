@@ -1,4 +1,5 @@
-"""ctypes binding of the C ABI in include/qe_attn.h (libqe_attn.so), without the torch extension.
+"""ctypes binding of the C ABI in include/qe_attn.h and include/qe_gemv.h (libqe_attn.so),
+without the torch extension.
 
 This is the binding a non-torch host (or a test that must go through the C ABI) uses. Tensor
 arguments may be torch tensors (their data_ptr is passed) or raw integer device addresses.
@@ -31,6 +32,9 @@ SIGNATURES = {
     "qe_attn_version": (ctypes.c_char_p, []),
     "qe_set_pdl_trigger": (None, [_I]),
     "qe_set_pdl_launch": (None, [_I]),
+    "qe_gemv_bf16": (_I, [_P, _P, _P, _I, _I, _I, _L, _L, _P]),
+    "qe_gemv_kparts": (_I, [_I, _I]),
+    "qe_hbm_read_probe": (_I, [_P, ctypes.c_size_t, _P, _P]),
 }
 
 HIP_SUCCESS = 0
@@ -114,3 +118,15 @@ def split_size(L: int, ns: int) -> int:
 
 def version() -> str:
     return load().qe_attn_version().decode()
+
+
+def gemv_bf16(W, x, out, nr, N, K, ldx, ldo, stream=None) -> int:
+    return load().qe_gemv_bf16(_ptr(W), _ptr(x), _ptr(out), nr, N, K, ldx, ldo, _stream(stream))
+
+
+def gemv_kparts(N: int, K: int) -> int:
+    return load().qe_gemv_kparts(N, K)
+
+
+def hbm_read_probe(buf, nbytes: int, sink, stream=None) -> int:
+    return load().qe_hbm_read_probe(_ptr(buf), nbytes, _ptr(sink), _stream(stream))

@@ -14,6 +14,7 @@
 #include <c10/hip/HIPStream.h>
 
 #include "qe_attn.h"
+#include "qe_gemv.h"
 
 namespace {
 const auto BF = torch::kBFloat16;
@@ -264,6 +265,41 @@ std::vector<int64_t> check_attn_decode(torch::Tensor q, torch::Tensor kc, torch:
   return {a.n, a.Hq, a.Hkv, a.max_len, a.NS, a.ldp, a.ldo};
 }
 
+// out[n, N] = x[n, K] @ W[N, K]^T for n = 1..8 rows: the reference's gemv_bf16 contract
+// (csrc/bindings.cpp:57-66): W contiguous bf16 [N, K], x and out row views, K % 8 == 0,
+// 16-byte aligned W and x rows.
+struct GemvArgs {
+  Rows X, O;
+  long N, K;
+};
+GemvArgs parse_gemv(const torch::Tensor& W, const torch::Tensor& x, const torch::Tensor& out,
+                    bool dev) {
+  chk(W, BF, "W", dev);
+  const auto X = rows(x, BF, "x", dev), O = rows(out, BF, "out", dev);
+  TORCH_CHECK(W.dim() == 2 && X.w == W.size(1) && O.w == W.size(0) && X.n == O.n,
+              "gemv_bf16: W [N, K], x [n, K], out [n, N]");
+  TORCH_CHECK(X.n >= 1 && X.n <= 8, "1..8 rows");
+  TORCH_CHECK(W.size(1) % 8 == 0, "K must be a multiple of 8");
+  chk16(W, W.size(1), "W");
+  chk16(x, X.ld, "x");
+  return {X, O, W.size(0), W.size(1)};
+}
+
+void gemv_bf16(torch::Tensor W, torch::Tensor x, torch::Tensor out) {
+  const auto a = parse_gemv(W, x, out, true);
+  TORCH_CHECK(x.device() == W.device() && out.device() == W.device(),
+              "W, x and out must be on one device");
+  const c10::DeviceGuard guard(W.device());
+  raise_on(qe_gemv_bf16(W.data_ptr(), x.data_ptr(), out.data_ptr(), a.X.n, (int)a.N, (int)a.K,
+                        a.X.ld, a.O.ld, stream_of(W)),
+           "qe_gemv_bf16");
+}
+
+std::vector<int64_t> check_gemv_bf16(torch::Tensor W, torch::Tensor x, torch::Tensor out) {
+  const auto a = parse_gemv(W, x, out, false);
+  return {a.X.n, a.N, a.K, a.X.ld, a.O.ld};
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "MI355X (gfx950) gated-attention decode ops with qengine._C's signatures";
   m.def("attn_prep", &attn_prep);
@@ -290,4 +326,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "validate attn_prep_decode arguments without launching");
   m.def("_check_attn_decode", &check_attn_decode,
         "validate attn_decode arguments without launching");
+  m.def("gemv_bf16", &gemv_bf16, "out[n, N] = x[n, K] @ W[N, K]^T, n = 1..8 (W, x, out)");
+  m.def("_check_gemv_bf16", &check_gemv_bf16, "validate gemv_bf16 arguments without launching");
 }

@@ -1,5 +1,5 @@
 """CPU tests of the drop-in boundary: the C-ABI library loads and exports every entry point that
-include/qe_attn.h declares, the C ABI rejects out-of-range arguments before launching anything,
+include/*.h declares, the C ABI rejects out-of-range arguments before launching anything,
 and the torch extension enforces the reference's validation contract
 (reference csrc/bindings.cpp:15-30,147-183). No kernel runs here."""
 import random
@@ -10,21 +10,26 @@ import pytest
 import torch
 
 ROOT = Path(__file__).resolve().parents[1]
-HEADER = ROOT / "include" / "qe_attn.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 BF, F32, I32 = torch.bfloat16, torch.float32, torch.int32
 D = 256
 INVALID = 1  # hipErrorInvalidValue
 
 
 def declared_symbols():
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"\b(qe_\w+)\s*\(", text)))
+    """Every qe_* entry point declared in include/*.h (comments stripped)."""
+    syms = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        syms |= set(re.findall(r"\b(qe_\w+)\s*\(", text))
+    return sorted(syms)
 
 
 def test_header_declares_the_path():
     syms = declared_symbols()
     for s in ("qe_attn_prep", "qe_attn_decode", "qe_attn_decode_partials",
-              "qe_attn_decode_combine", "qe_attn_split_size", "qe_attn_version"):
+              "qe_attn_decode_combine", "qe_attn_split_size", "qe_attn_version", "qe_gemv_bf16",
+              "qe_gemv_kparts", "qe_hbm_read_probe"):
         assert s in syms
 
 
@@ -255,3 +260,60 @@ def test_prep_decode_contract(native):
     with pytest.raises(RuntimeError, match="rows"):
         C._check_attn_prep_decode(qg[:2], k[:2], v[:2], qnw, knw, inv, a["pos"], a["q"][:2],
                                   a["kc"], a["vc"], a["part_o"], a["part_ml"], a["out"])
+
+
+# ------------------------------------------------------------------ gemv_bf16 (basic.cu:99-155)
+@pytest.mark.parametrize("kw,why", [
+    (dict(nr=0), "no rows"), (dict(nr=9), "more than 8 rows"), (dict(K=12), "K % 8"),
+    (dict(K=0), "empty rows"), (dict(N=0), "no outputs"), (dict(W=A + 8), "unaligned W"),
+    (dict(x=A + 2), "unaligned x"), (dict(ldx=5112), "ldx < K"), (dict(ldx=5124), "ldx % 8"),
+    (dict(ldo=100), "ldo < N"), (dict(out=None), "null out"),
+    (dict(K=1 << 27), "tile beyond 32-bit buffer offsets"),
+    (dict(nr=8, ldx=1 << 29), "activation rows beyond 32-bit buffer offsets"),
+])
+def test_capi_gemv_rejects(capi, kw, why):
+    a = dict(W=A, x=A, out=A, nr=1, N=14336, K=5120, ldx=5120, ldo=14336)
+    a.update(kw)
+    r = capi.load().qe_gemv_bf16(a["W"], a["x"], a["out"], a["nr"], a["N"], a["K"], a["ldx"],
+                                 a["ldo"], None)
+    assert r == INVALID, why
+
+
+def test_gemv_kparts():
+    """k-parts per 16-row tile: more for small N, never below 8 MFMA k-steps per part, and a
+    function of (N, K) only (so every row count reduces in the same order)."""
+    import qengine_amd.capi as capi
+    assert capi.gemv_kparts(248320, 5120) == 1      # lm_head: 15,520 row tiles
+    assert capi.gemv_kparts(14336, 5120) == 4       # attention in_proj: 896 tiles
+    assert capi.gemv_kparts(5120, 6144) == 4        # o_proj: 320 tiles
+    assert capi.gemv_kparts(40000, 5120) == 2       # 2,500 tiles
+    assert capi.gemv_kparts(5120, 768) == 1         # 3 blocks of 256 k: parts keep >= 2 blocks
+    assert capi.gemv_kparts(5120, 1024) == 2
+    assert capi.gemv_kparts(7, 64) == 1
+    assert capi.gemv_kparts(0, 64) == 0
+
+
+def test_gemv_contract(native):
+    """gemv_bf16 accepts the engine's layout (weights [N, K], a row view of the activations in a
+    wider buffer, a row view of the output) and rejects what the reference rejects."""
+    C = native
+    W = torch.zeros(1000, 1024, dtype=BF)
+    xb = torch.zeros(5, 1024 + 16, dtype=BF)
+    ob = torch.zeros(5, 1000 + 8, dtype=BF)
+    assert list(C._check_gemv_bf16(W, xb[:, :1024], ob[:, :1000])) == [5, 1000, 1024, 1040, 1008]
+    assert list(C._check_gemv_bf16(W, xb[0, :1024], ob[0, :1000]))[:3] == [1, 1000, 1024]
+    with pytest.raises(RuntimeError, match="1..8 rows"):
+        C._check_gemv_bf16(W, torch.zeros(9, 1024, dtype=BF), torch.zeros(9, 1000, dtype=BF))
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        C._check_gemv_bf16(torch.zeros(8, 12, dtype=BF), torch.zeros(1, 12, dtype=BF),
+                           torch.zeros(1, 8, dtype=BF))
+    with pytest.raises(RuntimeError, match="gemv_bf16"):
+        C._check_gemv_bf16(W, xb[:, :1024], ob[:4, :1000])
+    with pytest.raises(RuntimeError, match="contiguous"):
+        C._check_gemv_bf16(W.t(), xb[:, :1000], ob[:, :1000])
+    with pytest.raises(RuntimeError, match="wrong"):
+        C._check_gemv_bf16(W.float(), xb[:, :1024], ob[:, :1000])
+    with pytest.raises(RuntimeError, match="aligned"):
+        C._check_gemv_bf16(W, xb[:, 1:1025], ob[:, :1000])
+    with pytest.raises(RuntimeError, match="GPU"):
+        C.gemv_bf16(W, xb[:, :1024], ob[:, :1000])
