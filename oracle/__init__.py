@@ -12,6 +12,10 @@ Parity status per function (each is pinned by checks in ``tests/test_oracle.py``
                                                          invariants, bf16 rounding model)
   gemv_exact, gemv_bound, gemv_bf16_ref               -> pinned (brute-force loops, one-hot and
                                                          identity closed forms, NaN, the bound)
+  step_oracle: embed, residual_rmsnorm1p, swiglu, argmax, accept, commit, mtp_select
+                                                      -> pinned (closed forms, torch's own ops,
+                                                         hand-worked step scenarios)
 """
 from .attn_oracle import *  # noqa: F401,F403
 from .gemv_oracle import gemv_bf16_ref, gemv_bound, gemv_exact  # noqa: F401
+from . import step_oracle  # noqa: F401

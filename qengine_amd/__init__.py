@@ -21,6 +21,8 @@ except ImportError as exc:  # pragma: no cover - exercised only on an unbuilt tr
     ) from exc
 
 from ._C import (  # noqa: E402,F401
+    accept,
+    argmax,
     attn_decode,
     attn_decode_combine,
     attn_decode_partials,
@@ -28,10 +30,17 @@ from ._C import (  # noqa: E402,F401
     attn_prep,
     attn_prep_chunk,
     attn_prep_decode,
+    commit,
+    embed,
     gemv_bf16,
+    l2_persist_limit,
+    mtp_select,
+    rmsnorm1p,
     set_pdl_launch,
     set_pdl_trigger,
     split_size,
+    stream_window,
+    swiglu,
     version,
 )
 

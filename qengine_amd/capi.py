@@ -1,5 +1,5 @@
-"""ctypes binding of the C ABI in include/qe_attn.h and include/qe_gemv.h (libqe_attn.so),
-without the torch extension.
+"""ctypes binding of the C ABI in include/qe_attn.h, include/qe_gemv.h and include/qe_step.h
+(libqe_attn.so), without the torch extension.
 
 This is the binding a non-torch host (or a test that must go through the C ABI) uses. Tensor
 arguments may be torch tensors (their data_ptr is passed) or raw integer device addresses.
@@ -35,6 +35,15 @@ SIGNATURES = {
     "qe_gemv_bf16": (_I, [_P, _P, _P, _I, _I, _I, _L, _L, _P]),
     "qe_gemv_kparts": (_I, [_I, _I]),
     "qe_hbm_read_probe": (_I, [_P, ctypes.c_size_t, _P, _P]),
+    "qe_embed": (_I, [_P, _P, _P, _I, _I, _I, _L, _P]),
+    "qe_rmsnorm1p": (_I, [_P, _P, _P, _P, _I, _I, _L, _L, _L, _F, _P]),
+    "qe_swiglu": (_I, [_P, _P, _I, _I, _L, _L, _P]),
+    "qe_argmax": (_I, [_P, _I, _I, _L, _P, _P, _I, _P, _P, _P]),
+    "qe_accept": (_I, [_P, _P, _I, _P, _P, _P, _I, _P]),
+    "qe_commit": (_I, [_P, _P, _P, _P, _I, _P]),
+    "qe_mtp_select": (_I, [_P, _P, _I, _P, _L, _P, _I, _P, _P, _P]),
+    "qe_l2_persist_limit": (_I, [ctypes.c_size_t]),
+    "qe_stream_access_window": (_I, [ctypes.c_size_t, ctypes.c_size_t, _F, _P]),
 }
 
 HIP_SUCCESS = 0
@@ -130,3 +139,13 @@ def gemv_kparts(N: int, K: int) -> int:
 
 def hbm_read_probe(buf, nbytes: int, sink, stream=None) -> int:
     return load().qe_hbm_read_probe(_ptr(buf), nbytes, _ptr(sink), _stream(stream))
+
+
+def rmsnorm1p(x, delta, w, out, rows, H, ldx, ldd, ldo, eps, stream=None) -> int:
+    return load().qe_rmsnorm1p(_ptr(x), _ptr(delta), _ptr(w), _ptr(out), rows, H, ldx, ldd, ldo,
+                               eps, _stream(stream))
+
+
+def argmax(x, rows, n, ldx, pv, pi, nb, out, idmap=None, stream=None) -> int:
+    return load().qe_argmax(_ptr(x), rows, n, ldx, _ptr(pv), _ptr(pi), nb, _ptr(out), _ptr(idmap),
+                            _stream(stream))

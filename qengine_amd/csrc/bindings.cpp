@@ -15,6 +15,7 @@
 
 #include "qe_attn.h"
 #include "qe_gemv.h"
+#include "qe_step.h"
 
 namespace {
 const auto BF = torch::kBFloat16;
@@ -300,6 +301,172 @@ std::vector<int64_t> check_gemv_bf16(torch::Tensor W, torch::Tensor x, torch::Te
   return {a.X.n, a.N, a.K, a.X.ld, a.O.ld};
 }
 
+// ---- the rest of a decode step (reference csrc/bindings.cpp:33-55,68-136,186-188) ----------
+// Each parse_* validates like the reference; dev = false skips the device requirement so the
+// _check_* twins can run the contract on a machine without a GPU.
+
+struct EmbedArgs {
+  Rows O;
+  long V;
+};
+EmbedArgs parse_embed(const torch::Tensor& table, const torch::Tensor& tok,
+                      const torch::Tensor& out, bool dev) {
+  chk(table, BF, "table", dev);
+  TORCH_CHECK((!dev || tok.is_cuda()) && tok.scalar_type() == I32, "tok must be int32 on the GPU");
+  const auto O = rows(out, BF, "out", dev);
+  TORCH_CHECK(table.dim() == 2 && O.w == table.size(1) && tok.numel() >= O.n,
+              "embed: table [V, H], out [n, H], tok >= n ids");
+  return {O, table.size(0)};
+}
+void embed(torch::Tensor table, torch::Tensor tok, torch::Tensor out) {
+  const auto a = parse_embed(table, tok, out, true);
+  const c10::DeviceGuard guard(out.device());
+  raise_on(qe_embed(table.data_ptr(), tok.data_ptr<int>(), out.data_ptr(), a.O.n, (int)a.O.w,
+                    (int)a.V, a.O.ld, stream_of(out)),
+           "qe_embed");
+}
+
+struct NormArgs {
+  Rows X, O;
+  long ldd;
+  const void* d;
+};
+NormArgs parse_rmsnorm1p(const torch::Tensor& x, const c10::optional<torch::Tensor>& delta,
+                         const torch::Tensor& w, const torch::Tensor& out, bool dev) {
+  chk(w, BF, "w", dev);
+  const auto X = rows(x, BF, "x", dev), O = rows(out, BF, "out", dev);
+  TORCH_CHECK(X.w == w.numel() && O.w == X.w && O.n == X.n, "rmsnorm1p: x [n, H], w [H], out [n, H]");
+  long ldd = 0;
+  const void* d = nullptr;
+  if (delta.has_value()) {
+    const auto D = rows(*delta, BF, "delta", dev);
+    TORCH_CHECK(D.n == X.n && D.w == X.w, "delta must match x");
+    ldd = D.ld;
+    d = delta->data_ptr();
+  }
+  return {X, O, ldd, d};
+}
+void rmsnorm1p(torch::Tensor x, c10::optional<torch::Tensor> delta, torch::Tensor w,
+               torch::Tensor out, double eps) {
+  const auto a = parse_rmsnorm1p(x, delta, w, out, true);
+  const c10::DeviceGuard guard(x.device());
+  raise_on(qe_rmsnorm1p(x.data_ptr(), a.d, w.data_ptr(), out.data_ptr(), a.X.n, (int)a.X.w, a.X.ld,
+                        a.ldd, a.O.ld, (float)eps, stream_of(x)),
+           "qe_rmsnorm1p");
+}
+
+void swiglu(torch::Tensor gu, torch::Tensor out) {
+  const auto G = rows(gu, BF, "gu", true), O = rows(out, BF, "out", true);
+  TORCH_CHECK(G.w == 2 * O.w && G.n == O.n, "swiglu: gu [n, 2I], out [n, I]");
+  const c10::DeviceGuard guard(gu.device());
+  raise_on(qe_swiglu(gu.data_ptr(), out.data_ptr(), O.n, (int)O.w, G.ld, O.ld, stream_of(gu)),
+           "qe_swiglu");
+}
+
+struct ArgmaxArgs {
+  Rows X;
+  int nb;
+  const int* idmap;
+};
+ArgmaxArgs parse_argmax(const torch::Tensor& x, const torch::Tensor& ws_v,
+                        const torch::Tensor& ws_i, const torch::Tensor& out,
+                        const c10::optional<torch::Tensor>& idmap, bool dev) {
+  const auto X = rows(x, BF, "x", dev);
+  chk(ws_v, F32, "ws_v", dev);
+  chk(ws_i, I32, "ws_i", dev);
+  chk(out, I32, "out", dev);
+  const int nb = (int)(ws_v.numel() / X.n);
+  TORCH_CHECK(ws_v.numel() == ws_i.numel() && nb >= 1 && out.numel() >= X.n,
+              "argmax: ws_v/ws_i of rows*nb entries, out >= rows");
+  const int* mp = nullptr;
+  if (idmap.has_value()) {
+    chk(*idmap, I32, "idmap", dev);
+    TORCH_CHECK(idmap->numel() == X.w, "idmap must have one id per column of x");
+    mp = idmap->data_ptr<int>();
+  }
+  return {X, nb, mp};
+}
+void argmax(torch::Tensor x, torch::Tensor ws_v, torch::Tensor ws_i, torch::Tensor out,
+            c10::optional<torch::Tensor> idmap) {
+  const auto a = parse_argmax(x, ws_v, ws_i, out, idmap, true);
+  const c10::DeviceGuard guard(x.device());
+  raise_on(qe_argmax(x.data_ptr(), a.X.n, (int)a.X.w, a.X.ld, ws_v.data_ptr<float>(),
+                     ws_i.data_ptr<int>(), a.nb, out.data_ptr<int>(), a.idmap, stream_of(x)),
+           "qe_argmax");
+}
+
+void parse_accept(const torch::Tensor& in_tok, const torch::Tensor& am, int64_t n,
+                  const torch::Tensor& ctl, const torch::Tensor& next_tok,
+                  const torch::Tensor& log, bool dev) {
+  for (auto* t : {&in_tok, &am, &ctl, &next_tok, &log}) chk(*t, I32, "int buffer", dev);
+  TORCH_CHECK(n >= 1 && n <= 8, "accept: 1..8 rows");
+  TORCH_CHECK(in_tok.numel() > n && am.numel() >= n && next_tok.numel() >= n && ctl.numel() >= 24,
+              "accept: in_tok > n, am and next_tok >= n, ctl >= 24 entries");
+}
+void accept(torch::Tensor in_tok, torch::Tensor am, int64_t n, torch::Tensor ctl,
+            torch::Tensor next_tok, torch::Tensor log) {
+  parse_accept(in_tok, am, n, ctl, next_tok, log, true);
+  const c10::DeviceGuard guard(ctl.device());
+  raise_on(qe_accept(in_tok.data_ptr<int>(), am.data_ptr<int>(), (int)n, ctl.data_ptr<int>(),
+                     next_tok.data_ptr<int>(), log.data_ptr<int>(), (int)log.numel(),
+                     stream_of(ctl)),
+           "qe_accept");
+}
+
+void parse_commit(const torch::Tensor& ctl, const torch::Tensor& in_tok, const torch::Tensor& am,
+                  const torch::Tensor& drafts, int64_t k, bool dev) {
+  for (auto* t : {&ctl, &in_tok, &am, &drafts}) chk(*t, I32, "int buffer", dev);
+  TORCH_CHECK(k >= 0 && in_tok.numel() > k && drafts.numel() >= k && ctl.numel() >= 4,
+              "commit: in_tok > k, drafts >= k entries");
+}
+void commit(torch::Tensor ctl, torch::Tensor in_tok, torch::Tensor am, torch::Tensor drafts,
+            int64_t k) {
+  parse_commit(ctl, in_tok, am, drafts, k, true);
+  const c10::DeviceGuard guard(ctl.device());
+  raise_on(qe_commit(ctl.data_ptr<int>(), in_tok.data_ptr<int>(), am.data_ptr<int>(),
+                     drafts.data_ptr<int>(), (int)k, stream_of(ctl)),
+           "qe_commit");
+}
+
+struct SelectArgs {
+  const void* sp;
+  void* dp;
+  long lds;
+  int H;
+};
+SelectArgs parse_mtp_select(const torch::Tensor& ctl, const torch::Tensor& mpos,
+                            const c10::optional<torch::Tensor>& src,
+                            const c10::optional<torch::Tensor>& dst,
+                            const c10::optional<torch::Tensor>& mtp_am,
+                            const c10::optional<torch::Tensor>& draft0, bool dev) {
+  chk(ctl, I32, "ctl", dev);
+  chk(mpos, I32, "mpos", dev);
+  SelectArgs a{nullptr, nullptr, 0, 0};
+  if (src.has_value()) {
+    TORCH_CHECK(dst.has_value(), "mtp_select: src needs dst");
+    const auto S = rows(*src, BF, "src", dev);
+    chk(*dst, BF, "dst", dev);
+    TORCH_CHECK(dst->numel() == S.w, "dst must hold one row of src");
+    a = {src->data_ptr(), dst->data_ptr(), S.ld, (int)S.w};
+  }
+  if (draft0.has_value()) {
+    TORCH_CHECK(mtp_am.has_value(), "mtp_select: draft0 needs mtp_am");
+    chk(*draft0, I32, "draft0", dev);
+    chk(*mtp_am, I32, "mtp_am", dev);
+  }
+  return a;
+}
+void mtp_select(torch::Tensor ctl, torch::Tensor mpos, int64_t off,
+                c10::optional<torch::Tensor> src, c10::optional<torch::Tensor> dst,
+                c10::optional<torch::Tensor> mtp_am, c10::optional<torch::Tensor> draft0) {
+  const auto a = parse_mtp_select(ctl, mpos, src, dst, mtp_am, draft0, true);
+  const c10::DeviceGuard guard(ctl.device());
+  raise_on(qe_mtp_select(ctl.data_ptr<int>(), mpos.data_ptr<int>(), (int)off, a.sp, a.lds, a.dp,
+                         a.H, mtp_am.has_value() ? mtp_am->data_ptr<int>() : nullptr,
+                         draft0.has_value() ? draft0->data_ptr<int>() : nullptr, stream_of(ctl)),
+           "qe_mtp_select");
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "MI355X (gfx950) gated-attention decode ops with qengine._C's signatures";
   m.def("attn_prep", &attn_prep);
@@ -327,5 +494,44 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("_check_attn_decode", &check_attn_decode,
         "validate attn_decode arguments without launching");
   m.def("gemv_bf16", &gemv_bf16, "out[n, N] = x[n, K] @ W[N, K]^T, n = 1..8 (W, x, out)");
+  m.def("embed", &embed, "out[r] = table[tok[r]] (zeros for ids outside the table)");
+  m.def("rmsnorm1p", &rmsnorm1p, py::arg("x"), py::arg("delta"), py::arg("w"), py::arg("out"),
+        py::arg("eps"));
+  m.def("swiglu", &swiglu, "out = bf16(bf16(silu(gate)) * up) per row of gu = [gate | up]");
+  m.def("argmax", &argmax, py::arg("x"), py::arg("ws_v"), py::arg("ws_i"), py::arg("out"),
+        py::arg("idmap") = py::none());
+  m.def("accept", &accept);
+  m.def("commit", &commit);
+  m.def("mtp_select", &mtp_select, py::arg("ctl"), py::arg("mpos"), py::arg("off"),
+        py::arg("src") = py::none(), py::arg("dst") = py::none(), py::arg("mtp_am") = py::none(),
+        py::arg("draft0") = py::none());
+  m.def("l2_persist_limit", [](int64_t b) { raise_on(qe_l2_persist_limit((size_t)b), "qe_l2_persist_limit"); },
+        "no-op on gfx950 (no persisting-L2 control; kept for import compatibility)");
+  m.def("stream_window",
+        [](int64_t base, int64_t bytes, double hit) {
+          raise_on(qe_stream_access_window((uintptr_t)base, (size_t)bytes, (float)hit, nullptr),
+                   "qe_stream_access_window");
+        },
+        "no-op on gfx950 (no access-policy window; kept for import compatibility)");
+  m.def("_check_embed", [](torch::Tensor t, torch::Tensor k, torch::Tensor o) {
+    const auto a = parse_embed(t, k, o, false);
+    return std::vector<int64_t>{a.O.n, a.O.w, a.V, a.O.ld};
+  });
+  m.def("_check_rmsnorm1p", [](torch::Tensor x, c10::optional<torch::Tensor> d, torch::Tensor w,
+                               torch::Tensor o) {
+    const auto a = parse_rmsnorm1p(x, d, w, o, false);
+    return std::vector<int64_t>{a.X.n, a.X.w, a.X.ld, a.ldd, a.O.ld};
+  });
+  m.def("_check_argmax", [](torch::Tensor x, torch::Tensor v, torch::Tensor i, torch::Tensor o,
+                            c10::optional<torch::Tensor> idmap) {
+    const auto a = parse_argmax(x, v, i, o, idmap, false);
+    return std::vector<int64_t>{a.X.n, a.X.w, a.X.ld, a.nb};
+  }, py::arg("x"), py::arg("ws_v"), py::arg("ws_i"), py::arg("out"), py::arg("idmap") = py::none());
+  m.def("_check_accept", [](torch::Tensor t, torch::Tensor am, int64_t n, torch::Tensor c,
+                            torch::Tensor nt, torch::Tensor lg) {
+    parse_accept(t, am, n, c, nt, lg, false);
+  });
+  m.def("_check_commit", [](torch::Tensor c, torch::Tensor t, torch::Tensor am, torch::Tensor d,
+                            int64_t k) { parse_commit(c, t, am, d, k, false); });
   m.def("_check_gemv_bf16", &check_gemv_bf16, "validate gemv_bf16 arguments without launching");
 }

@@ -317,3 +317,68 @@ def test_gemv_contract(native):
         C._check_gemv_bf16(W, xb[:, 1:1025], ob[:, :1000])
     with pytest.raises(RuntimeError, match="GPU"):
         C.gemv_bf16(W, xb[:, :1024], ob[:, :1000])
+
+
+# ------------------------------------------------------------------ the rest of the step (basic.cu)
+@pytest.mark.parametrize("fn,args,why", [
+    ("qe_embed", (A, A, A, 0, 64, 10, 64, None), "no rows"),
+    ("qe_embed", (A, A, A, 1, 64, 10, 32, None), "ldo < H"),
+    ("qe_embed", (None, A, A, 1, 64, 10, 64, None), "null table"),
+    ("qe_rmsnorm1p", (A, None, A, A, 0, 64, 64, 0, 64, 1e-6, None), "no rows"),
+    ("qe_rmsnorm1p", (A, A, A, A, 1, 64, 64, 32, 64, 1e-6, None), "ldd < H with delta"),
+    ("qe_swiglu", (A, A, 1, 64, 100, 64, None), "ldg < 2I"),
+    ("qe_argmax", (A, 1, 100, 50, A, A, 4, A, None, None), "ldx < n"),
+    ("qe_argmax", (A, 1, 100, 100, A, A, 0, A, None, None), "no partials"),
+    ("qe_accept", (A, A, 9, A, A, A, 10, None), "more than 8 rows"),
+    ("qe_accept", (A, A, 0, A, A, A, 10, None), "no rows"),
+    ("qe_commit", (A, A, A, None, 2, None), "drafts missing"),
+    ("qe_mtp_select", (A, A, 0, A, 64, None, 64, None, None, None), "src without dst"),
+    ("qe_mtp_select", (A, A, 0, None, 0, None, 0, None, A, None), "draft0 without mtp_am"),
+])
+def test_capi_step_ops_reject(capi, fn, args, why):
+    assert getattr(capi.load(), fn)(*args) == INVALID, why
+
+
+def test_capi_l2_controls_succeed_without_a_gpu(capi):
+    lib = capi.load()
+    assert lib.qe_l2_persist_limit(60 << 20) == 0
+    assert lib.qe_stream_access_window(0, 0, 0.0, None) == 0
+
+
+def test_step_ops_contract(native):
+    """The reference's checks for embed / rmsnorm1p / argmax / accept / commit
+    (csrc/bindings.cpp:33-55,68-124), exercised without a GPU."""
+    C = native
+    tab = torch.zeros(100, 64, dtype=BF)
+    ob = torch.zeros(3, 72, dtype=BF)
+    assert list(C._check_embed(tab, torch.zeros(3, dtype=I32), ob[:, :64])) == [3, 64, 100, 72]
+    with pytest.raises(RuntimeError, match="tok"):
+        C._check_embed(tab, torch.zeros(3, dtype=torch.int64), ob[:, :64])
+    with pytest.raises(RuntimeError, match="embed"):
+        C._check_embed(tab, torch.zeros(2, dtype=I32), ob[:, :64])
+    x = torch.zeros(4, 5120, dtype=BF)
+    w = torch.zeros(5120, dtype=BF)
+    assert list(C._check_rmsnorm1p(x, None, w, x)) == [4, 5120, 5120, 0, 5120]
+    assert list(C._check_rmsnorm1p(x, x, w, x))[3] == 5120
+    with pytest.raises(RuntimeError, match="rmsnorm1p"):
+        C._check_rmsnorm1p(x, None, w[:100], x)
+    with pytest.raises(RuntimeError, match="delta"):
+        C._check_rmsnorm1p(x, x[:2], w, x)
+    lg = torch.zeros(5, 1000, dtype=BF)
+    assert list(C._check_argmax(lg, torch.zeros(5 * 256), torch.zeros(5 * 256, dtype=I32),
+                                torch.zeros(5, dtype=I32))) == [5, 1000, 1000, 256]
+    with pytest.raises(RuntimeError, match="argmax"):
+        C._check_argmax(lg, torch.zeros(5 * 256), torch.zeros(5 * 128, dtype=I32),
+                        torch.zeros(5, dtype=I32))
+    with pytest.raises(RuntimeError, match="idmap"):
+        C._check_argmax(lg, torch.zeros(5), torch.zeros(5, dtype=I32), torch.zeros(5, dtype=I32),
+                        torch.zeros(999, dtype=I32))
+    ints = lambda k: torch.zeros(k, dtype=I32)  # noqa: E731
+    C._check_accept(ints(9), ints(8), 8, ints(24), ints(8), ints(100))
+    with pytest.raises(RuntimeError, match="accept"):
+        C._check_accept(ints(8), ints(8), 8, ints(24), ints(8), ints(100))   # in_tok must hold n+1
+    with pytest.raises(RuntimeError, match="accept"):
+        C._check_accept(ints(9), ints(8), 8, ints(16), ints(8), ints(100))   # ctl >= 24
+    C._check_commit(ints(24), ints(8), ints(8), ints(7), 7)
+    with pytest.raises(RuntimeError, match="commit"):
+        C._check_commit(ints(24), ints(7), ints(8), ints(7), 7)
