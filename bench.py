@@ -268,6 +268,7 @@ def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
 
     res.update(bench_prefill(torch, C, steps, warmup))
     res.update(bench_gemv(torch, C, qa, steps, warmup))
+    res.update(bench_step_ops(torch, C, steps, warmup))
     return res
 
 
@@ -306,6 +307,55 @@ def bench_gemv(torch, C, qa, steps: int, warmup: int) -> dict:
     res["hbm_read_probe_2GiB"] = {"us": round(us, 2), "GBps": round(nbytes / (us * 1e3), 1),
                                   "hbm_frac": round(nbytes / (us * 1e3) / HBM_PEAK_GBS, 4)}
     del buf
+    return res
+
+
+def bench_step_ops(torch, C, steps: int, warmup: int) -> dict:
+    """The rest of a decode step at the reference model's shapes (hidden 5120, intermediate
+    17408, vocab 248320): embed, rmsnorm1p with the fused residual, swiglu, argmax (two launches),
+    accept + commit. Each is 16 calls per graph on rotating buffers; values are per call. These
+    kernels are launch- and latency-bound (2-20 KB per row, 0.5 MB per logits row)."""
+    dev, BF, I32 = "cuda", torch.bfloat16, torch.int32
+    gen = torch.Generator(device=dev).manual_seed(4)
+    H, I, V, nl = 5120, 17408, 248320, 16
+    res = {}
+
+    def per_call(fn):
+        return round(time_fn_graph(torch, fn, steps, warmup) * 1e3 / nl, 3)
+
+    tab = torch.randn(V, H, device=dev, generator=gen).to(BF)
+    tok = torch.randint(0, V, (8,), device=dev, generator=gen, dtype=I32)
+    outs = [torch.empty(8, H, dtype=BF, device=dev) for _ in range(nl)]
+    for n in (1, 5):
+        res[f"embed_rows{n}"] = {"us": per_call(lambda: [C.embed(tab, tok, o[:n]) for o in outs])}
+    del tab
+    xs = [torch.randn(8, H, device=dev, generator=gen).to(BF) for _ in range(nl)]
+    ds = [torch.randn(8, H, device=dev, generator=gen).to(BF) for _ in range(nl)]
+    w = torch.randn(H, device=dev, generator=gen).to(BF)
+    for n in (1, 5):
+        res[f"rmsnorm1p_residual_rows{n}"] = {
+            "us": per_call(lambda: [C.rmsnorm1p(x[:n], d[:n], w, o[:n], 1e-6)
+                                    for x, d, o in zip(xs, ds, outs)])}
+    gus = [torch.randn(8, 2 * I, device=dev, generator=gen).to(BF) for _ in range(nl)]
+    acts = [torch.empty(8, I, dtype=BF, device=dev) for _ in range(nl)]
+    for n in (1, 5):
+        us = per_call(lambda: [C.swiglu(g[:n], a[:n]) for g, a in zip(gus, acts)])
+        res[f"swiglu_rows{n}"] = {"us": us, "GBps": round(n * I * 6 / (us * 1e3), 1)}
+    del gus, acts
+    lgs = [torch.randn(8, V, device=dev, generator=gen).to(BF) for _ in range(nl)]
+    wv, wi = torch.empty(8 * 256, device=dev), torch.empty(8 * 256, dtype=I32, device=dev)
+    am = torch.empty(8, dtype=I32, device=dev)
+    for n in (1, 5):
+        us = per_call(lambda: [C.argmax(lg[:n], wv[:n * 256], wi[:n * 256], am) for lg in lgs])
+        res[f"argmax_vocab_rows{n}"] = {"us": us, "GBps": round(n * V * 2 / (us * 1e3), 1)}
+    del lgs
+    ctl = torch.zeros(32, dtype=I32, device=dev)
+    in_tok = torch.zeros(9, dtype=I32, device=dev)
+    nt, dr = torch.zeros(8, dtype=I32, device=dev), torch.zeros(8, dtype=I32, device=dev)
+    log = torch.zeros(1 << 20, dtype=I32, device=dev)
+    res["accept_commit_rows5"] = {"us": per_call(lambda: [(C.accept(in_tok, am, 5, ctl, nt, log),
+                                                           C.commit(ctl, in_tok, am, dr, 4))
+                                                          for _ in range(nl)])}
     return res
 
 
@@ -396,6 +446,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only BASELINE config 5 (chunked prefill); prints its timing as JSON")
+    ap.add_argument("--step-ops-only", action="store_true",
+                    help="only embed / rmsnorm1p / swiglu / argmax / accept+commit, as JSON")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the in_proj / o_proj GEMV and the HBM read probe, as JSON")
     ap.add_argument("--no-configs", action="store_true",
@@ -430,6 +482,9 @@ def main():
         return
     if args.gemv_only:
         print(json.dumps(bench_gemv(torch, C, qa, args.steps, args.warmup)))
+        return
+    if args.step_ops_only:
+        print(json.dumps(bench_step_ops(torch, C, args.steps, args.warmup)))
         return
     lengths = [int(x) for x in args.lengths.split(",") if x]
     if HEADLINE_L not in lengths:
