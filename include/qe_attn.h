@@ -100,6 +100,34 @@ hipError_t qe_attn_prefill(const void* q, const void* kc, const void* vc, const 
  * multiply and shift for the division by NS). Returns 0 for L < 1, L >= 2^23 or NS < 1. */
 int qe_attn_split_size(int L, int NS);
 
+/* The fp8 KV cache (no counterpart in the reference, whose cache is bf16: python/qengine/
+ * engine.py:419): kc8/vc8 are [Hkv][max_len][256] E4M3FN codes (one byte per value, OCP fp8, the
+ * format gfx950's cvt instructions use) with one scale per cache: a code c stands for c * scale.
+ * Halves the bytes the decode streams. */
+
+/* qe_attn_prep writing the fp8 cache: a K or V value x is stored as the code nearest to
+ * x * (1 / scale) (fp32 product, round to nearest even, saturated at +-448; NaN stays NaN).
+ * Valid as qe_attn_prep, plus k_scale, v_scale positive and finite. */
+hipError_t qe_attn_prep_fp8(const void* qg, const void* k, const void* v, long ldp,
+                            const void* qnw, const void* knw, const float* inv_freq,
+                            const int* pos, void* q_out, void* kc8, void* vc8, int n, int Hq,
+                            int Hkv, int max_len, int rd, float eps, float k_scale, float v_scale,
+                            hipStream_t stream);
+
+/* qe_attn_decode over the fp8 cache: the same attention on the dequantized values (k_scale
+ * scales every score, v_scale the attention output before its bf16 rounding). Row t of an n-row
+ * call is bit-identical to a 1-row call. Valid as qe_attn_decode with (Hq/Hkv)*n <= 32. */
+hipError_t qe_attn_decode_fp8(const void* q, const void* kc8, const void* vc8, const int* pos,
+                              const void* qg, long ldp, float* part_o, float* part_ml, void* out,
+                              long ldo, int n, int Hq, int Hkv, int max_len, int NS, float scale,
+                              float k_scale, float v_scale, hipStream_t stream);
+
+/* First half of qe_attn_decode_fp8 (the partials are not yet multiplied by v_scale). */
+hipError_t qe_attn_decode_fp8_partials(const void* q, const void* kc8, const void* vc8,
+                                       const int* pos, float* part_o, float* part_ml, int n,
+                                       int Hq, int Hkv, int max_len, int NS, float scale,
+                                       float k_scale, hipStream_t stream);
+
 /* Version string of this library. */
 const char* qe_attn_version(void);
 

@@ -25,11 +25,14 @@ from ._C import (  # noqa: E402,F401
     argmax,
     attn_decode,
     attn_decode_combine,
+    attn_decode_fp8,
+    attn_decode_fp8_partials,
     attn_decode_partials,
     attn_prefill,
     attn_prep,
     attn_prep_chunk,
     attn_prep_decode,
+    attn_prep_fp8,
     commit,
     embed,
     gemv_bf16,

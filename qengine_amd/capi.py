@@ -32,6 +32,11 @@ SIGNATURES = {
     "qe_attn_version": (ctypes.c_char_p, []),
     "qe_set_pdl_trigger": (None, [_I]),
     "qe_set_pdl_launch": (None, [_I]),
+    "qe_attn_prep_fp8": (_I, [_P, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F,
+                              _F, _P]),
+    "qe_attn_decode_fp8": (_I, [_P, _P, _P, _P, _P, _L, _P, _P, _P, _L, _I, _I, _I, _I, _I, _F, _F,
+                                _F, _P]),
+    "qe_attn_decode_fp8_partials": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P]),
     "qe_gemv_bf16": (_I, [_P, _P, _P, _I, _I, _I, _L, _L, _P]),
     "qe_gemv_kparts": (_I, [_I, _I]),
     "qe_hbm_read_probe": (_I, [_P, ctypes.c_size_t, _P, _P]),

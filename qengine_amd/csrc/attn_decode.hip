@@ -173,6 +173,79 @@ __device__ __forceinline__ void wait_and_compute(const VTile& b, const u32x4_t* 
   }
 }
 
+// fp8 KV (E4M3FN codes, 256-byte rows): the same tile and the same arithmetic after an exact
+// conversion to bf16. K: 8 LDS-DMA loads (instruction j covers rows 4j..4j+3; lane i fetches the
+// 16-byte chunk that belongs in slot 64j + i, chunks XOR-swizzled by row as for bf16); V: 16
+// register loads of 8 bytes, the dims and rows of the bf16 layout (VTile), converted before use.
+struct VTile8 {
+  u32x2_t v[8][2];  // V rows P(g4, e), dims 128h + 8c + [0, 8), as fp8 codes
+};
+
+__device__ __forceinline__ void load_tile8(VTile8& b, u32x4_t* ks_lds, __amdgpu_buffer_rsrc_t krs,
+                                           __amdgpu_buffer_rsrc_t vrs, int p0, int lane, int c,
+                                           int g4) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int r = 4 * j + (lane >> 4);
+    const int q = (lane & 15) ^ (r & 15);
+    buffer_load16_to_lds(krs, (uint32_t)(p0 + r) * HD + q * 16, ks_lds + 64 * j);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      b.v[e][h] = buffer_load8_stream(
+          vrs, (uint32_t)(p0 + 16 * (e >> 2) + 4 * g4 + (e & 3)) * HD + 128 * h + 8 * c);
+}
+
+// S^T = K Q^T from an fp8 K tile in LDS: lane (c, g4) reads the 8 codes of row 16T + c, dims
+// [32ks + 8g4, +8) (half of the swizzled 16-byte chunk 2ks + g4/2) and converts them to the bf16
+// A operand of qk_tile.
+template <int NT>
+__device__ __forceinline__ void qk_tile8(const u32x4_t* k_lds, const bf16x8_t (&qb)[NT][8], int c,
+                                         int g4, f32x4_t (&sacc)[NT][2]) {
+  const char* base = reinterpret_cast<const char*>(k_lds);
+#pragma unroll
+  for (int T = 0; T < 2; ++T) {
+#pragma unroll
+    for (int ct = 0; ct < NT; ++ct) sacc[ct][T] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const int r = 16 * T + c;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const int chunk = (2 * ks + (g4 >> 1)) ^ (r & 15);
+      const u32x2_t w = *reinterpret_cast<const u32x2_t*>(base + (r * 16 + chunk) * 16 + (g4 & 1) * 8);
+      const bf16x8_t kop = as_bf16x8(fp8x8_to_bf16x8(w));
+#pragma unroll
+      for (int ct = 0; ct < NT; ++ct) sacc[ct][T] = mfma16x16x32(kop, qb[ct][ks], sacc[ct][T]);
+    }
+  }
+}
+
+template <int NT>
+__device__ __forceinline__ void wait_and_compute8(const VTile8& b, const u32x4_t* ks_lds, int p0,
+                                                  int Lmin, const int (&Lcol)[NT],
+                                                  const bf16x8_t (&qb)[NT][8], float scale_log2,
+                                                  int c, int g4, float (&m)[NT], float (&l)[NT],
+                                                  f32x4_t (&acc)[NT][16]) {
+  vmcnt_wait<16>();  // the 8 K loads were issued before the 16 V loads
+  wave_lds_fence();
+  f32x4_t sacc[NT][2];
+  qk_tile8<NT>(ks_lds, qb, c, g4, sacc);
+  wave_lds_fence();  // this tile's K reads happen before the next tile's LDS-DMA writes
+  u32x4_t pb_hi[NT], pb_lo[NT];
+  if (p0 + TILE > Lmin)
+    tile::softmax_tile<NT, true, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
+  else
+    tile::softmax_tile<NT, false, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    u32x4_t vr[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vr[e] = fp8x8_to_bf16x8(b.v[e][hh]);
+    tile::pv_half<NT, true>(vr, hh, pb_hi, pb_lo, acc);
+  }
+}
+
 // LDS: per-wave K tiles during the loop; reused for the cross-wave merge afterwards.
 template <int WAVES>
 constexpr int lds_k_bytes() { return WAVES * TILE * HD * 2; }  // 16 KB per wave
@@ -367,7 +440,8 @@ __device__ __forceinline__ void fused_prep_compute(const PrepRegs<NT>& r, const 
 // Every workgroup whose slices hold a position pos+t writes cache row pos+t itself, before any of
 // its waves loads a tile, so it never depends on another workgroup's write (when two workgroups
 // write one row, they write the same bits). kc/vc are written here, so they are not __restrict__.
-template <int NT, bool FUSED = false, bool MULTI = true, int WAVES = waves_for<NT>()>
+template <int NT, bool FUSED = false, bool MULTI = true, bool KV8 = false,
+          int WAVES = waves_for<NT>()>
 __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_eu(NT == 1 && !FUSED ? 2 : 1, 2)))
 attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf16* vc,
                      const int* __restrict__ pos_ptr, float* __restrict__ part_o,
@@ -413,8 +487,10 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
 
   __shared__ __attribute__((aligned(16))) char lds[lds_k_bytes<WAVES>()];
   __shared__ float s_m[WAVES][16 * NT], s_l[WAVES][16 * NT];
+  static_assert(!(FUSED && KV8), "the fused prep writes a bf16 cache");
   u32x4_t* ks_lds = reinterpret_cast<u32x4_t*>(lds) + w * TILE * ROW_CHUNKS;
-  const size_t head_off = (size_t)g * max_len * HD;
+  constexpr int ELEM = KV8 ? 1 : 2;  // bytes per cache value
+  const size_t head_off = (size_t)g * max_len * HD * ELEM;  // bytes
 
   if constexpr (FUSED) {
     // rows t in [t_lo, t_hi) sit at positions this workgroup reads: their K/V rows are written here
@@ -444,9 +520,11 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
 #pragma unroll
     for (int ct = 0; ct < NT; ++ct)
       Lcol[ct] = in_pass(ct * 16 + c, grp, P) ? min(pos0 + trow[ct] + 1, max_len) : 0;
-    const uint32_t bytes = (uint32_t)P.end * (uint32_t)(HD * 2);  // loads past the slice read 0
-    const __amdgpu_buffer_rsrc_t krs = make_rsrc_uniform(kc + head_off, bytes);
-    const __amdgpu_buffer_rsrc_t vrs = make_rsrc_uniform(vc + head_off, bytes);
+    const uint32_t bytes = (uint32_t)P.end * (uint32_t)(HD * ELEM);  // loads past the slice read 0
+    const __amdgpu_buffer_rsrc_t krs =
+        make_rsrc_uniform(reinterpret_cast<const char*>(kc) + head_off, bytes);
+    const __amdgpu_buffer_rsrc_t vrs =
+        make_rsrc_uniform(reinterpret_cast<const char*>(vc) + head_off, bytes);
 
     float m[NT], l[NT];
     f32x4_t acc[NT][16];  // [8hh + i]: O^T dims 128hh + 32g4 + 8ii + i (tile::pv_half)
@@ -458,10 +536,18 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
       for (int a = 0; a < 16; ++a) acc[ct][a] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
 
-    VTile buf;
-    for (int p0 = P.beg + w * TILE; p0 < P.end; p0 += WAVES * TILE) {
-      load_tile(buf, ks_lds, krs, vrs, p0, lane, c, g4);
-      wait_and_compute<NT>(buf, ks_lds, p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
+    if constexpr (KV8) {
+      VTile8 buf;
+      for (int p0 = P.beg + w * TILE; p0 < P.end; p0 += WAVES * TILE) {
+        load_tile8(buf, ks_lds, krs, vrs, p0, lane, c, g4);
+        wait_and_compute8<NT>(buf, ks_lds, p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
+      }
+    } else {
+      VTile buf;
+      for (int p0 = P.beg + w * TILE; p0 < P.end; p0 += WAVES * TILE) {
+        load_tile(buf, ks_lds, krs, vrs, p0, lane, c, g4);
+        wait_and_compute<NT>(buf, ks_lds, p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
+      }
     }
 
     // ---- merge the waves of this workgroup in a fixed order and write the slice's partial
@@ -749,7 +835,7 @@ __global__ void __launch_bounds__(WAVE)
 attn_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml,
                     const int* __restrict__ pos_ptr, const __bf16* __restrict__ qg, long ldp,
                     __bf16* __restrict__ out, long ldo, int Hq, int max_len, int NS,
-                    NsDiv nd) {
+                    NsDiv nd, float v_scale) {
   const int h = blockIdx.x, t = blockIdx.y, z = blockIdx.z;
   const int lane = threadIdx.x, c16 = lane & 15, sg = lane >> 4;
   const size_t base = ((size_t)t * Hq + h) * NS;
@@ -816,7 +902,8 @@ attn_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ 
     __bf16* op = out + (size_t)t * ldo + (size_t)h * HD + dim;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float o = round_bf16(O[i] / L);  // attention output is a bf16 tensor
+      // attention output is a bf16 tensor (v_scale: the fp8 cache's V scale, else exactly 1)
+      const float o = round_bf16((O[i] / L) * v_scale);
       op[i] = f32_to_bf16(o * round_bf16(sigmoid_f32(gate[i])));
     }
   }
@@ -834,16 +921,29 @@ static hipError_t check_decode_shape(int n, int Hq, int Hkv, int max_len, int NS
   return hipSuccess;
 }
 
+// kv8: the cache is the fp8 KV format; k_scale multiplies every score (q . (code * k_scale)),
+// folded into the softmax scale.
 static hipError_t launch_partials(const void* q, const void* kc, const void* vc, const int* pos,
                                   float* part_o, float* part_ml, int n, int Hq, int Hkv,
-                                  int max_len, int NS, float scale, hipStream_t stream) {
+                                  int max_len, int NS, float scale, hipStream_t stream,
+                                  bool kv8 = false, float k_scale = 1.f) {
   const dim3 grid(max_slices(max_len, NS), Hkv);
   const NsDiv nd = ns_div(NS);
-  const float scale_log2 = scale * 1.4426950408889634f;
+  const float scale_log2 = scale * 1.4426950408889634f * k_scale;
   const int NT = ((Hq / Hkv) * n + 15) / 16;
   const auto* Q = static_cast<const __bf16*>(q);
   const auto* K = static_cast<const __bf16*>(kc);
   const auto* V = static_cast<const __bf16*>(vc);
+  if (kv8) {
+    if (NT > 2) return hipErrorInvalidValue;  // the multi-row cols kernel reads bf16 only
+    if (NT == 1 && n == 1)
+      attn_partials_kernel<1, false, false, true><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{});
+    else if (NT == 1)
+      attn_partials_kernel<1, false, true, true><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{});
+    else
+      attn_partials_kernel<2, false, true, true><<<grid, dim3(waves_for<2>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{});
+    return hipGetLastError();
+  }
   // NT = 1, 2: every wave holds all column tiles (measured fastest at 1-5 rows, GQA 6).
   // NT = 3, 4: one subset wave per column tile (the one-tile kernel would spill: 2.3-2.8x slower).
   switch (NT) {
@@ -862,10 +962,10 @@ static hipError_t launch_partials(const void* q, const void* kc, const void* vc,
 
 static hipError_t launch_combine(const float* part_o, const float* part_ml, const int* pos,
                                  const void* qg, long ldp, void* out, long ldo, int n, int Hq,
-                                 int max_len, int NS, hipStream_t stream) {
+                                 int max_len, int NS, hipStream_t stream, float v_scale = 1.f) {
   attn_combine_kernel<<<dim3(Hq, n, HD / COMBINE_DIMS), dim3(WAVE), 0, stream>>>(
       part_o, part_ml, pos, static_cast<const __bf16*>(qg), ldp, static_cast<__bf16*>(out), ldo,
-      Hq, max_len, NS, ns_div(NS));
+      Hq, max_len, NS, ns_div(NS), v_scale);
   return hipGetLastError();
 }
 
@@ -908,6 +1008,38 @@ extern "C" hipError_t qe_attn_decode(const void* q, const void* kc, const void* 
   if (e != hipSuccess) return e;
   return qe_attn_decode_combine(part_o, part_ml, pos, qg, ldp, out, ldo, n, Hq, max_len, NS,
                                 stream);
+}
+
+static bool kv_scales_ok(float k_scale, float v_scale) {
+  return k_scale > 0.f && v_scale > 0.f && k_scale < INFINITY && v_scale < INFINITY;
+}
+
+extern "C" hipError_t qe_attn_decode_fp8_partials(const void* q, const void* kc8, const void* vc8,
+                                                  const int* pos, float* part_o, float* part_ml,
+                                                  int n, int Hq, int Hkv, int max_len, int NS,
+                                                  float scale, float k_scale,
+                                                  hipStream_t stream) {
+  hipError_t e = check_decode_shape(n, Hq, Hkv, max_len, NS);
+  if (e != hipSuccess) return e;
+  if ((Hq / Hkv) * n > 32 || !kv_scales_ok(k_scale, 1.f)) return hipErrorInvalidValue;
+  if (!aligned16(q) || !aligned16(kc8) || !aligned16(vc8) || !aligned16(part_o) || !pos ||
+      !part_ml)
+    return hipErrorInvalidValue;
+  return launch_partials(q, kc8, vc8, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, scale,
+                         stream, true, k_scale);
+}
+
+extern "C" hipError_t qe_attn_decode_fp8(const void* q, const void* kc8, const void* vc8,
+                                         const int* pos, const void* qg, long ldp, float* part_o,
+                                         float* part_ml, void* out, long ldo, int n, int Hq,
+                                         int Hkv, int max_len, int NS, float scale, float k_scale,
+                                         float v_scale, hipStream_t stream) {
+  if (!kv_scales_ok(k_scale, v_scale) || !qg || !out) return hipErrorInvalidValue;
+  hipError_t e = qe_attn_decode_fp8_partials(q, kc8, vc8, pos, part_o, part_ml, n, Hq, Hkv,
+                                             max_len, NS, scale, k_scale, stream);
+  if (e != hipSuccess) return e;
+  return launch_combine(part_o, part_ml, pos, qg, ldp, out, ldo, n, Hq, max_len, NS, stream,
+                        v_scale);
 }
 
 extern "C" hipError_t qe_attn_prep(const void* qg, const void* k, const void* v, long ldp,

@@ -9,6 +9,8 @@
 //
 // The _check_* functions run the same validation without the device requirement and without a
 // launch, so the contract can be exercised on a machine without a GPU.
+#include <cmath>
+
 #include <torch/extension.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
@@ -54,6 +56,14 @@ void chk16(const torch::Tensor& t, long ld, const char* name) {
               " must be 16-byte aligned rows");
 }
 
+// The fp8 KV cache: E4M3FN codes, as torch.float8_e4m3fn or raw uint8 bytes.
+void chk_kv8(const torch::Tensor& t, const char* name, bool dev) {
+  if (dev) TORCH_CHECK(t.is_cuda(), name, " must be a GPU tensor");
+  TORCH_CHECK(t.scalar_type() == torch::kFloat8_e4m3fn || t.scalar_type() == torch::kByte, name,
+              " must be float8_e4m3fn (or uint8 codes), got ", t.scalar_type());
+  TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+}
+
 void chk_pos(const torch::Tensor& pos, bool dev) {
   TORCH_CHECK((!dev || pos.is_cuda()) && pos.scalar_type() == I32 && pos.numel() >= 1,
               "pos must be an int32 GPU tensor with at least one element");
@@ -72,14 +82,19 @@ PrepArgs parse_prep(const torch::Tensor& qg, const torch::Tensor& k, const torch
                     const torch::Tensor& qnw, const torch::Tensor& knw,
                     const torch::Tensor& inv_freq, const torch::Tensor& pos,
                     const torch::Tensor& q_out, const torch::Tensor& kc, const torch::Tensor& vc,
-                    bool dev, int max_rows = 8) {
+                    bool dev, int max_rows = 8, bool kv8 = false) {
   auto QG = rows(qg, BF, "qg", dev), K = rows(k, BF, "k", dev), V = rows(v, BF, "v", dev);
   auto QO = rows(q_out, BF, "q_out", dev);
   TORCH_CHECK(QG.ld == K.ld && QG.ld == V.ld, "qg/k/v must share a row stride");
   chk(qnw, BF, "qnw", dev);
   chk(knw, BF, "knw", dev);
-  chk(kc, BF, "kc", dev);
-  chk(vc, BF, "vc", dev);
+  if (kv8) {
+    chk_kv8(kc, "kc", dev);
+    chk_kv8(vc, "vc", dev);
+  } else {
+    chk(kc, BF, "kc", dev);
+    chk(vc, BF, "vc", dev);
+  }
   chk(inv_freq, F32, "inv_freq", dev);
   chk_pos(pos, dev);
   TORCH_CHECK(kc.dim() == 3 && kc.size(2) == HD, "head_dim 256 only");
@@ -104,10 +119,15 @@ struct DecodeArgs {
 DecodeArgs parse_decode(const torch::Tensor& q, const torch::Tensor& kc, const torch::Tensor& vc,
                         const torch::Tensor& pos, const torch::Tensor& qg,
                         const torch::Tensor& part_o, const torch::Tensor& part_ml,
-                        const torch::Tensor& out, bool dev) {
+                        const torch::Tensor& out, bool dev, bool kv8 = false) {
   auto Qr = rows(q, BF, "q", dev), QG = rows(qg, BF, "qg", dev), O = rows(out, BF, "out", dev);
-  chk(kc, BF, "kc", dev);
-  chk(vc, BF, "vc", dev);
+  if (kv8) {
+    chk_kv8(kc, "kc", dev);
+    chk_kv8(vc, "vc", dev);
+  } else {
+    chk(kc, BF, "kc", dev);
+    chk(vc, BF, "vc", dev);
+  }
   chk(part_o, F32, "part_o", dev);
   chk(part_ml, F32, "part_ml", dev);
   chk_pos(pos, dev);
@@ -127,7 +147,8 @@ DecodeArgs parse_decode(const torch::Tensor& q, const torch::Tensor& kc, const t
                   QG.w == (long)Hq * 2 * HD,
               "part_ml must be [>=n, Hq, NS, 2]; out width Hq*256; qg width Hq*512");
   TORCH_CHECK(n >= 1 && n <= 8, "decode takes 1..8 rows");
-  TORCH_CHECK((Hq / Hkv) * n <= 64, "GQA group size * rows must be <= 64");
+  TORCH_CHECK((Hq / Hkv) * n <= (kv8 ? 32 : 64),
+              "GQA group size * rows must be <= ", kv8 ? 32 : 64, kv8 ? " with the fp8 cache" : "");
   TORCH_CHECK(NS >= 1, "part_o needs at least one split");
   return {n, Hq, Hkv, max_len, NS, QG.ld, O.ld};
 }
@@ -264,6 +285,57 @@ std::vector<int64_t> check_attn_decode(torch::Tensor q, torch::Tensor kc, torch:
                                        torch::Tensor part_ml, torch::Tensor out) {
   const auto a = parse_decode(q, kc, vc, pos, qg, part_o, part_ml, out, false);
   return {a.n, a.Hq, a.Hkv, a.max_len, a.NS, a.ldp, a.ldo};
+}
+
+// ---- fp8 KV cache (no reference counterpart: the reference cache is bf16, engine.py:419) ------
+// attn_prep / attn_decode over a cache of E4M3FN codes with per-cache scales: a stored code c
+// means c * scale; prep stores round-to-nearest-even(x / scale), saturated at +-448.
+void kv_scales(double k_scale, double v_scale) {
+  TORCH_CHECK(k_scale > 0 && v_scale > 0 && std::isfinite(k_scale) && std::isfinite(v_scale),
+              "k_scale and v_scale must be positive and finite");
+}
+
+void attn_prep_fp8(torch::Tensor qg, torch::Tensor k, torch::Tensor v, torch::Tensor qnw,
+                   torch::Tensor knw, torch::Tensor inv_freq, torch::Tensor pos, torch::Tensor q_out,
+                   torch::Tensor kc8, torch::Tensor vc8, double eps, double k_scale,
+                   double v_scale) {
+  const auto a = parse_prep(qg, k, v, qnw, knw, inv_freq, pos, q_out, kc8, vc8, true, 8, true);
+  kv_scales(k_scale, v_scale);
+  const c10::DeviceGuard guard(qg.device());
+  raise_on(qe_attn_prep_fp8(qg.data_ptr(), k.data_ptr(), v.data_ptr(), a.ldp, qnw.data_ptr(),
+                            knw.data_ptr(), inv_freq.data_ptr<float>(), pos.data_ptr<int>(),
+                            q_out.data_ptr(), kc8.data_ptr(), vc8.data_ptr(), a.n, a.Hq, a.Hkv,
+                            a.max_len, a.rd, (float)eps, (float)k_scale, (float)v_scale,
+                            stream_of(qg)),
+           "qe_attn_prep_fp8");
+}
+
+void attn_decode_fp8(torch::Tensor q, torch::Tensor kc8, torch::Tensor vc8, torch::Tensor pos,
+                     torch::Tensor qg, torch::Tensor part_o, torch::Tensor part_ml,
+                     torch::Tensor out, double k_scale, double v_scale) {
+  const auto a = parse_decode(q, kc8, vc8, pos, qg, part_o, part_ml, out, true, true);
+  kv_scales(k_scale, v_scale);
+  const c10::DeviceGuard guard(q.device());
+  raise_on(qe_attn_decode_fp8(q.data_ptr(), kc8.data_ptr(), vc8.data_ptr(), pos.data_ptr<int>(),
+                              qg.data_ptr(), a.ldp, part_o.data_ptr<float>(),
+                              part_ml.data_ptr<float>(), out.data_ptr(), a.ldo, a.n, a.Hq, a.Hkv,
+                              a.max_len, a.NS, 1.0f / 16.0f, (float)k_scale, (float)v_scale,
+                              stream_of(q)),
+           "qe_attn_decode_fp8");
+}
+
+void attn_decode_fp8_partials(torch::Tensor q, torch::Tensor kc8, torch::Tensor vc8,
+                              torch::Tensor pos, torch::Tensor qg, torch::Tensor part_o,
+                              torch::Tensor part_ml, torch::Tensor out, double k_scale,
+                              double v_scale) {
+  const auto a = parse_decode(q, kc8, vc8, pos, qg, part_o, part_ml, out, true, true);
+  kv_scales(k_scale, v_scale);
+  const c10::DeviceGuard guard(q.device());
+  raise_on(qe_attn_decode_fp8_partials(q.data_ptr(), kc8.data_ptr(), vc8.data_ptr(),
+                                       pos.data_ptr<int>(), part_o.data_ptr<float>(),
+                                       part_ml.data_ptr<float>(), a.n, a.Hq, a.Hkv, a.max_len, a.NS,
+                                       1.0f / 16.0f, (float)k_scale, stream_of(q)),
+           "qe_attn_decode_fp8_partials");
 }
 
 // out[n, N] = x[n, K] @ W[N, K]^T for n = 1..8 rows: the reference's gemv_bf16 contract
@@ -494,6 +566,20 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("_check_attn_decode", &check_attn_decode,
         "validate attn_decode arguments without launching");
   m.def("gemv_bf16", &gemv_bf16, "out[n, N] = x[n, K] @ W[N, K]^T, n = 1..8 (W, x, out)");
+  m.def("attn_prep_fp8", &attn_prep_fp8,
+        "attn_prep writing the fp8 KV cache (qg, k, v, qnw, knw, inv_freq, pos, q_out, kc8, vc8, "
+        "eps, k_scale, v_scale)");
+  m.def("attn_decode_fp8", &attn_decode_fp8,
+        "attn_decode over the fp8 KV cache (q, kc8, vc8, pos, qg, part_o, part_ml, out, k_scale, "
+        "v_scale)");
+  m.def("attn_decode_fp8_partials", &attn_decode_fp8_partials,
+        "split-KV partials of attn_decode_fp8 (same arguments)");
+  m.def("_check_attn_decode_fp8", [](torch::Tensor q, torch::Tensor kc8, torch::Tensor vc8,
+                                     torch::Tensor pos, torch::Tensor qg, torch::Tensor po,
+                                     torch::Tensor pml, torch::Tensor out) {
+    const auto a = parse_decode(q, kc8, vc8, pos, qg, po, pml, out, false, true);
+    return std::vector<int64_t>{a.n, a.Hq, a.Hkv, a.max_len, a.NS};
+  });
   m.def("embed", &embed, "out[r] = table[tok[r]] (zeros for ids outside the table)");
   m.def("rmsnorm1p", &rmsnorm1p, py::arg("x"), py::arg("delta"), py::arg("w"), py::arg("out"),
         py::arg("eps"));

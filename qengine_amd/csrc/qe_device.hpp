@@ -176,6 +176,40 @@ __device__ __forceinline__ u32x4_t buffer_load16_stream(__amdgpu_buffer_rsrc_t r
       u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, CPOL_NT));
 }
 
+// 8 bytes (non-temporal), e.g. eight fp8 cache values.
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32x2_t buffer_load8_stream(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(
+      u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, (int)byte_off, 0, CPOL_NT));
+}
+
+// ---------------------------------------------------------------------------- fp8 (OCP E4M3FN)
+// The fp8 KV cache stores E4M3FN codes (1 sign, 4 exponent bits with bias 7, 3 mantissa bits;
+// S.1111.111 is NaN; largest finite 448). gfx950's v_cvt_pk_f32_fp8 decodes this format
+// (checked for all 256 codes on MI355X) and v_cvt_pk_fp8_f32 encodes it with round-to-nearest-
+// even and no saturation (|x| >= 480 becomes NaN), so the encoder clamps to +-448 first.
+
+// Eight fp8 codes (little-endian in w) -> eight bf16 (as 4 packed pairs). Every E4M3 value is a
+// bf16 value, so keeping the upper half of the fp32 is exact.
+__device__ __forceinline__ uint32_t fp8x2_to_bf16x2_lo(uint32_t w) {  // codes in bytes 0, 1
+  const auto f = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  return __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u);
+}
+__device__ __forceinline__ uint32_t fp8x2_to_bf16x2_hi(uint32_t w) {  // codes in bytes 2, 3
+  const auto f = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  return __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u);
+}
+__device__ __forceinline__ u32x4_t fp8x8_to_bf16x8(u32x2_t w) {
+  return u32x4_t{fp8x2_to_bf16x2_lo(w[0]), fp8x2_to_bf16x2_hi(w[0]), fp8x2_to_bf16x2_lo(w[1]),
+                 fp8x2_to_bf16x2_hi(w[1])};
+}
+
+// x -> fp8 code: round to nearest even, saturate at +-448, NaN stays NaN.
+__device__ __forceinline__ uint8_t f32_to_fp8(float x) {
+  const float c = x != x ? x : fminf(fmaxf(x, -448.0f), 448.0f);
+  return (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(c, 0.0f, 0, false) & 0xff);
+}
+
 // 16 bytes per lane from a buffer straight into LDS (gfx950 LDS DMA, non-temporal): lane i of the
 // wave writes lds_base + 16*i. lds_base must be wave-uniform. The compiler does not order later
 // LDS reads after this write: wait with vmcnt_wait() first.

@@ -1,0 +1,128 @@
+"""GPU tests of the fp8 KV cache path (attn_prep_fp8, attn_decode_fp8) against the CPU oracle:
+  * prep stores exactly the oracle's codes of the bf16 prep's K and V rows (value-exact), and the
+    same q_out bits;
+  * with scales of 1 the fp8 decode is bit-identical to the bf16 decode run on the dequantized
+    cache (the MFMA inputs are the same bf16 values), which pins the fp8 tile layout and the
+    conversion;
+  * with any scales it is within the decode tolerance of the oracle's attention over the
+    dequantized cache (per element |out-ref| <= 2^-6|ref| + 2e-3, max-abs 2e-2, mean-abs 2e-3);
+  * rows of a multi-row call are bit-identical to 1-row calls."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from attn_cases import BF, D, attn_close, decode_case
+from oracle import kv8_oracle as K8
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+F8 = torch.float8_e4m3fn
+
+
+def quantize_cache(kc: torch.Tensor, scale: float) -> torch.Tensor:
+    """bf16 cache -> fp8 codes (CPU oracle), as a float8_e4m3fn tensor."""
+    codes = K8.encode(kc.float().numpy(), scale)
+    return torch.from_numpy(codes).view(F8)
+
+
+def run_fp8(C, q, qg, kc8, vc8, pos, ns, ks, vs):
+    n = q.shape[0]
+    hq = q.shape[1] // D
+    out = torch.empty(n, hq * D, dtype=BF, device=DEV)
+    po = torch.empty(n, hq, ns, D, device=DEV)
+    pml = torch.empty(n, hq, ns, 2, device=DEV)
+    C.attn_decode_fp8(q.to(DEV), kc8.to(DEV), vc8.to(DEV),
+                      torch.tensor([pos], dtype=torch.int32, device=DEV), qg.to(DEV), po, pml,
+                      out, ks, vs)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def run_bf16(C, q, qg, kc, vc, pos, ns):
+    n = q.shape[0]
+    hq = q.shape[1] // D
+    out = torch.empty(n, hq * D, dtype=BF, device=DEV)
+    po = torch.empty(n, hq, ns, D, device=DEV)
+    pml = torch.empty(n, hq, ns, 2, device=DEV)
+    C.attn_decode(q.to(DEV), kc.to(DEV), vc.to(DEV),
+                  torch.tensor([pos], dtype=torch.int32, device=DEV), qg.to(DEV), po, pml, out)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+@pytest.mark.parametrize("hq,hkv,n,pos,max_len,ns", [
+    (24, 4, 1, 1023, 1024, 32), (24, 4, 5, 4096, 4101, 64), (8, 2, 3, 30, 100, 4),
+    (24, 4, 2, 16382, 16384, 64), (24, 4, 4, 2046, 2100, 64), (32, 8, 4, 700, 1000, 16)])
+def test_fp8_scale_one_equals_bf16_on_the_dequantized_cache(native, hq, hkv, n, pos, max_len, ns):
+    case = decode_case(seed=pos + n, hq=hq, hkv=hkv, pos=pos, n=n, max_len=max_len)
+    kc8, vc8 = quantize_cache(case.kc, 1.0), quantize_cache(case.vc, 1.0)
+    kd = K8.dequantize(kc8.view(torch.uint8), 1.0).to(BF)  # exact: every code is a bf16 value
+    vd = K8.dequantize(vc8.view(torch.uint8), 1.0).to(BF)
+    a = run_fp8(native, case.q, case.qg, kc8, vc8, case.pos, ns, 1.0, 1.0)
+    b = run_bf16(native, case.q, case.qg, kd, vd, case.pos, ns)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("ks,vs", [(1.0, 1.0), (0.5, 0.25), (0.037, 0.011), (3.0, 2.0)])
+@pytest.mark.parametrize("n,pos,max_len", [(1, 4095, 4096), (5, 4096, 4101), (2, 300, 20000)])
+def test_fp8_decode_vs_oracle(native, ks, vs, n, pos, max_len):
+    case = decode_case(seed=n * 31 + pos, hq=24, hkv=4, pos=pos, n=n, max_len=max_len)
+    kc8, vc8 = quantize_cache(case.kc, ks), quantize_cache(case.vc, vs)
+    out = run_fp8(native, case.q, case.qg, kc8, vc8, case.pos, 64, ks, vs)
+    kd = K8.dequantize(kc8.view(torch.uint8), ks)
+    vd = K8.dequantize(vc8.view(torch.uint8), vs)
+    ref = O.attn_decode(case.q, kd, vd, case.pos, case.qg, case.hq)
+    ok, mx, mean = attn_close(out, ref)
+    assert ok, (mx, mean)
+    for t in range(n):
+        o1 = run_fp8(native, case.q[t:t + 1], case.qg[t:t + 1], kc8, vc8, case.pos + t, 64, ks, vs)
+        assert torch.equal(o1[0], out[t]), t
+
+
+def test_fp8_decode_long_cache_16k(native):
+    """BASELINE cfg 2's 16k shape on the fp8 cache, 1 and 5 rows, vs the oracle."""
+    case = decode_case(seed=16, hq=24, hkv=4, pos=16379, n=5, max_len=16384)
+    ks, vs = 0.125, 0.125
+    kc8, vc8 = quantize_cache(case.kc, ks), quantize_cache(case.vc, vs)
+    out = run_fp8(native, case.q, case.qg, kc8, vc8, case.pos, 64, ks, vs)
+    ref = O.attn_decode(case.q, K8.dequantize(kc8.view(torch.uint8), ks),
+                        K8.dequantize(vc8.view(torch.uint8), vs), case.pos, case.qg, case.hq)
+    ok, mx, mean = attn_close(out, ref)
+    assert ok, (mx, mean)
+
+
+@pytest.mark.parametrize("ks,vs", [(1.0, 1.0), (0.05, 0.2)])
+def test_prep_fp8_writes_the_oracle_codes(native, ks, vs):
+    """Same q_out as attn_prep; the new K/V rows are the oracle's codes of the bf16 rows."""
+    C = native
+    hq, hkv, n, pos, max_len = 24, 4, 3, 500, 512
+    g = torch.Generator().manual_seed(int(ks * 1000))
+    proj = (torch.randn(n, hq * 2 * D + 2 * hkv * D, generator=g) * 3).to(BF).to(DEV)
+    qg, k, v = proj[:, : hq * 2 * D], proj[:, hq * 2 * D: hq * 2 * D + hkv * D], proj[:, hq * 2 * D + hkv * D:]
+    qnw = (torch.randn(D, generator=g) * 0.3).to(BF).to(DEV)
+    knw = (torch.randn(D, generator=g) * 0.3).to(BF).to(DEV)
+    inv = O.rope_inv_freq(1e7, 64).to(DEV)
+    p = torch.tensor([pos], dtype=torch.int32, device=DEV)
+    q_a, q_b = torch.empty(n, hq * D, dtype=BF, device=DEV), torch.empty(n, hq * D, dtype=BF, device=DEV)
+    kc = torch.zeros(hkv, max_len, D, dtype=BF, device=DEV)
+    vc = torch.zeros_like(kc)
+    kc8 = torch.zeros(hkv, max_len, D, dtype=torch.uint8, device=DEV).view(F8)
+    vc8 = torch.zeros_like(kc8)
+    C.attn_prep(qg, k, v, qnw, knw, inv, p, q_a, kc, vc, 1e-6)
+    C.attn_prep_fp8(qg, k, v, qnw, knw, inv, p, q_b, kc8, vc8, 1e-6, ks, vs)
+    torch.cuda.synchronize()
+    assert torch.equal(q_a, q_b)
+    rows = slice(pos, pos + n)
+    for cache, cache8, s in ((kc, kc8, ks), (vc, vc8, vs)):
+        want = K8.decode(K8.encode(cache[:, rows].float().cpu().numpy(), s))
+        got = K8.decode(cache8[:, rows].view(torch.uint8).cpu())
+        assert np.array_equal(got, want)
+        assert int(cache8.view(torch.uint8)[:, : pos].count_nonzero()) == 0  # nothing else written
+
+
+def test_fp8_rejects_wide_verify_shapes(native):
+    case = decode_case(seed=1, hq=24, hkv=4, pos=100, n=6, max_len=200)
+    kc8, vc8 = quantize_cache(case.kc, 1.0), quantize_cache(case.vc, 1.0)
+    with pytest.raises(RuntimeError, match="32"):
+        run_fp8(native, case.q, case.qg, kc8, vc8, case.pos, 8, 1.0, 1.0)
