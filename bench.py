@@ -83,6 +83,59 @@ class LayerSet:
                                         self.out)
 
 
+class LayerSet8(LayerSet):
+    """The same layer-calls on fp8 KV caches (E4M3FN codes drawn uniformly from the finite
+    codes, scale 1/16): half the bytes per position."""
+
+    def __init__(self, torch, C, L: int, ns: int, gen):
+        dev = "cuda"
+        BF = torch.bfloat16
+
+        def codes():
+            c = torch.randint(0, 256, (HKV, L, D), device=dev, generator=gen, dtype=torch.int32)
+            c = torch.where((c & 0x7F) == 0x7F, c ^ 1, c)  # no NaN codes
+            return c.to(torch.uint8).view(torch.float8_e4m3fn)
+        self.kc = [codes() for _ in range(LAYERS)]
+        self.vc = [codes() for _ in range(LAYERS)]
+        self.q = torch.randn(1, HQ * D, device=dev, generator=gen).to(BF)
+        self.qg = torch.randn(1, HQ * 2 * D, device=dev, generator=gen).to(BF)
+        self.out = torch.empty(1, HQ * D, dtype=BF, device=dev)
+        self.po = torch.empty(1, HQ, ns, D, device=dev)
+        self.pml = torch.empty(1, HQ, ns, 2, device=dev)
+        self.pos = torch.tensor([L - 1], dtype=torch.int32, device=dev)
+        self.C = C
+
+    def decode_all(self):
+        for k, v in zip(self.kc, self.vc):
+            self.C.attn_decode_fp8(self.q, k, v, self.pos, self.qg, self.po, self.pml, self.out,
+                                   1 / 16, 1 / 16)
+
+    def partials_all(self):
+        for k, v in zip(self.kc, self.vc):
+            self.C.attn_decode_fp8_partials(self.q, k, v, self.pos, self.qg, self.po, self.pml,
+                                            self.out, 1 / 16, 1 / 16)
+
+
+def bench_length_fp8(torch, C, qa, L: int, steps: int, warmup: int) -> dict:
+    """fp8 KV decode at KV length L: layer-call and partials-only µs; bytes = 2048*L (+ q)."""
+    ns = qa.default_splits(L, HKV)
+    nsets = max(1, math.ceil(ROTATE_BYTES / (LAYERS * L * 2048)))
+    gen = torch.Generator(device="cuda").manual_seed(L + 8)
+    sets = [LayerSet8(torch, C, L, ns, gen) for _ in range(nsets)]
+    full = [capture(torch, s.decode_all) for s in sets]
+    part = [capture(torch, s.partials_all) for s in sets]
+    us_layer = time_graphs(torch, full, steps, warmup) * 1e3 / LAYERS
+    us_part = time_graphs(torch, part, steps, warmup) * 1e3 / LAYERS
+    b_layer = 2048 * L + 36864
+    b_part = 2048 * L + 12288
+    del sets, full, part
+    torch.cuda.empty_cache()
+    return {"us_per_layer": round(us_layer, 3), "GBps": round(b_layer / (us_layer * 1e3), 1),
+            "partials_us": round(us_part, 3),
+            "partials_GBps": round(b_part / (us_part * 1e3), 1),
+            "partials_frac": round(b_part / (us_part * 1e3) / HBM_PEAK_GBS, 4)}
+
+
 def capture(torch, fn):
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -266,6 +319,8 @@ def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
                                       "GBps": round(alg_bytes_layer(La) / (us * 1e3), 1)}
     del kcs, vcs
 
+    for L in (4096, 16384, 32768, 131072):
+        res[f"fp8kv_decode_{L // 1024}k"] = bench_length_fp8(torch, C, qa, L, steps, warmup)
     res.update(bench_prefill(torch, C, steps, warmup))
     res.update(bench_gemv(torch, C, qa, steps, warmup))
     res.update(bench_step_ops(torch, C, steps, warmup))
@@ -446,6 +501,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only BASELINE config 5 (chunked prefill); prints its timing as JSON")
+    ap.add_argument("--fp8-only", action="store_true",
+                    help="only the fp8 KV decode sweep (4k-128k), as JSON")
     ap.add_argument("--step-ops-only", action="store_true",
                     help="only embed / rmsnorm1p / swiglu / argmax / accept+commit, as JSON")
     ap.add_argument("--gemv-only", action="store_true",
@@ -482,6 +539,11 @@ def main():
         return
     if args.gemv_only:
         print(json.dumps(bench_gemv(torch, C, qa, args.steps, args.warmup)))
+        return
+    if args.fp8_only:
+        print(json.dumps({f"fp8kv_decode_{L // 1024}k": bench_length_fp8(torch, C, qa, L, args.steps,
+                                                                          args.warmup)
+                          for L in (4096, 16384, 32768, 131072)}))
         return
     if args.step_ops_only:
         print(json.dumps(bench_step_ops(torch, C, args.steps, args.warmup)))
