@@ -324,6 +324,7 @@ def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
     res.update(bench_prefill(torch, C, steps, warmup))
     res.update(bench_gemv(torch, C, qa, steps, warmup))
     res.update(bench_step_ops(torch, C, steps, warmup))
+    res.update(bench_gdn(torch, C, steps, warmup))
     return res
 
 
@@ -411,6 +412,70 @@ def bench_step_ops(torch, C, steps: int, warmup: int) -> dict:
     res["accept_commit_rows5"] = {"us": per_call(lambda: [(C.accept(in_tok, am, 5, ctl, nt, log),
                                                            C.commit(ctl, in_tok, am, dr, 4))
                                                           for _ in range(nl)])}
+    return res
+
+
+GDN_HK, GDN_HV, GDN_LAYERS = 16, 48, 48
+
+
+def gdn_alg_bytes(n: int, pend: int, hk: int = GDN_HK, hv: int = GDN_HV) -> int:
+    """Algorithmic HBM bytes of one gdn_step_n call: the fp32 state read and written back (the
+    write only when rows are replayed), the replayed and the newly staged rows (k, v, decay,
+    beta in fp32), conv weights, the 3-position ring history and the n ring slots written, and
+    the bf16 rows qkv / z / b / a in and out."""
+    Cd, Vd = 2 * hk * 128 + hv * 128, hv * 128
+    state = hv * 128 * 128 * 4 * (2 if pend > 0 else 1)
+    staged = (pend + n) * hv * (128 + 128 + 2) * 4
+    conv = Cd * 4 * 2 + 3 * Cd * 2 + n * Cd * 2
+    rows = n * (Cd + Vd + 2 * hv) * 2 + n * Vd * 2
+    return state + staged + conv + rows + hv * 2 * 2 + 128 * 2
+
+
+def bench_gdn(torch, C, steps: int, warmup: int) -> dict:
+    """Gated DeltaNet step (gdn_step_n) at the reference model's shapes (Hk 16, Hv 48: 48 value
+    heads with a 128 x 128 fp32 state, 3 MB per layer), the way the reference times it
+    (bench/engine/micro_kernels.py:35-56): 48 layer-calls per graph on separate states, with
+    pending = n staged rows replayed by every call. Two graphs alternate over 2 x 48 states
+    (about 360 MB) so the 256 MB Infinity Cache cannot hold them; values are per call."""
+    dev, BF, I32 = "cuda", torch.bfloat16, torch.int32
+    hk, hv, nl = GDN_HK, GDN_HV, GDN_LAYERS
+    Cd, Vd = 2 * hk * 128 + hv * 128, hv * 128
+    w = Cd + Vd + 2 * hv
+    gen = torch.Generator(device=dev).manual_seed(5)
+    pr = (torch.randn(8, (w + 7) // 8 * 8, device=dev, generator=gen) * 0.5).to(BF)
+    qkv, z, b, a = pr[:, :Cd], pr[:, Cd:Cd + Vd], pr[:, Cd + Vd:Cd + Vd + hv], pr[:, Cd + Vd + hv:w]
+    conv_w = (torch.randn(Cd, 1, 4, device=dev, generator=gen) * 0.3).to(BF)
+    A_log = torch.zeros(hv, dtype=BF, device=dev)
+    dt = torch.zeros(hv, dtype=BF, device=dev)
+    nw = torch.ones(128, dtype=BF, device=dev)
+    out = torch.empty(8, Vd, dtype=BF, device=dev)
+
+    def layer():
+        return dict(ring=torch.zeros(16, Cd, dtype=BF, device=dev),
+                    S=torch.randn(hv, 128, 128, device=dev, generator=gen) * 0.01,
+                    st=[torch.zeros(8, hv, 128, device=dev), torch.zeros(8, hv, 128, device=dev),
+                        torch.zeros(8, hv, 2, device=dev)])
+
+    def call(Ld, n, ctl):
+        C.gdn_step_n(qkv[:n], z[:n], b[:n], a[:n], Ld["ring"], conv_w, A_log, dt, nw, Ld["S"],
+                     *Ld["st"], ctl, out[:n], hk, 1e-6)
+
+    res = {}
+    for n in (1, 4, 8):
+        sets = [[layer() for _ in range(nl)] for _ in range(2)]
+        prime = torch.tensor([100, 0, 0, 0, 0, 0, 0, 0], dtype=I32, device=dev)
+        ctl = torch.tensor([100, n, 0, 0, 0, 0, 0, 0], dtype=I32, device=dev)
+        for s in sets:  # stage n real rows in every layer, then time calls that replay them
+            for Ld in s:
+                call(Ld, n, prime)
+        graphs = [capture(torch, lambda s=s: [call(Ld, n, ctl) for Ld in s]) for s in sets]
+        us = time_graphs(torch, graphs, steps, warmup) * 1e3 / nl
+        nb = gdn_alg_bytes(n, n)
+        res[f"gdn_step_rows{n}"] = {"us": round(us, 3), "alg_bytes": nb,
+                                    "GBps": round(nb / (us * 1e3), 1),
+                                    "hbm_frac": round(nb / (us * 1e3) / HBM_PEAK_GBS, 4)}
+        del sets, graphs
+        torch.cuda.empty_cache()
     return res
 
 
@@ -505,6 +570,8 @@ def main():
                     help="only the fp8 KV decode sweep (4k-128k), as JSON")
     ap.add_argument("--step-ops-only", action="store_true",
                     help="only embed / rmsnorm1p / swiglu / argmax / accept+commit, as JSON")
+    ap.add_argument("--gdn-only", action="store_true",
+                    help="only the Gated DeltaNet step at the model's shapes, as JSON")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the in_proj / o_proj GEMV and the HBM read probe, as JSON")
     ap.add_argument("--no-configs", action="store_true",
@@ -547,6 +614,9 @@ def main():
         return
     if args.step_ops_only:
         print(json.dumps(bench_step_ops(torch, C, args.steps, args.warmup)))
+        return
+    if args.gdn_only:
+        print(json.dumps(bench_gdn(torch, C, args.steps, args.warmup)))
         return
     lengths = [int(x) for x in args.lengths.split(",") if x]
     if HEADLINE_L not in lengths:

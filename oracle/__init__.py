@@ -15,7 +15,14 @@ Parity status per function (each is pinned by checks in ``tests/test_oracle.py``
   step_oracle: embed, residual_rmsnorm1p, swiglu, argmax, accept, commit, mtp_select
                                                       -> pinned (closed forms, torch's own ops,
                                                          hand-worked step scenarios)
+  kv8_oracle: decode, encode, dequantize              -> pinned (torch's float8_e4m3fn, closed
+                                                         forms, ties, saturation)
+  gdn_oracle: conv_silu, gates, l2norm, delta_update, gated_rmsnorm, GdnLayer.step_n / keep
+                                                      -> pinned (HF transformers' qwen3_5 decode
+                                                         functions, HF's chunked delta rule, the
+                                                         fp64 matrix form, numpy convolution,
+                                                         closed forms, rollback invariants)
 """
 from .attn_oracle import *  # noqa: F401,F403
 from .gemv_oracle import gemv_bf16_ref, gemv_bound, gemv_exact  # noqa: F401
-from . import step_oracle  # noqa: F401
+from . import gdn_oracle, kv8_oracle, step_oracle  # noqa: F401

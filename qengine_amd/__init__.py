@@ -1,8 +1,9 @@
 """qengine_amd: MI355X-native (gfx950) gated-attention decode path for qengine.
 
-``qengine_amd._C`` exposes the reference's ``qengine._C`` attention ops with the same signatures
-(``attn_prep``, ``attn_decode``, plus the PDL switches as no-ops), backed by hand-written HIP
-kernels in ``libqe_attn.so`` (C ABI: ``include/qe_attn.h``). There is no CPU fallback: importing
+``qengine_amd._C`` exposes the reference's ``qengine._C`` ops with the same signatures
+(``attn_prep``, ``attn_decode``, the rest of the decode step, ``gdn_step_n``, plus the reference's
+PDL / L2 / GDN A/B switches as no-ops), backed by hand-written HIP kernels in ``libqe_attn.so``
+(C ABI: ``include/qe_*.h``). There is no CPU fallback: importing
 this package fails if the native libraries are not built.
 """
 from __future__ import annotations
@@ -35,10 +36,13 @@ from ._C import (  # noqa: E402,F401
     attn_prep_fp8,
     commit,
     embed,
+    gdn_step_n,
     gemv_bf16,
     l2_persist_limit,
     mtp_select,
     rmsnorm1p,
+    set_gdn_early,
+    set_gdn_phases,
     set_pdl_launch,
     set_pdl_trigger,
     split_size,

@@ -1,7 +1,7 @@
 """Build recipe for qengine_amd's native code (no setuptools, no hipify).
 
-  libqe_attn.so  : gfx950 HIP kernels + the C ABI of include/qe_attn.h, include/qe_gemv.h
-                   and include/qe_step.h (hipcc).
+  libqe_attn.so  : gfx950 HIP kernels + the C ABI of include/qe_attn.h, include/qe_gemv.h,
+                   include/qe_step.h and include/qe_gdn.h (hipcc).
   _C<ext>.so     : torch extension with the reference's op signatures (g++ against torch's
                    ROCm build), linked to libqe_attn.so through $ORIGIN.
 
@@ -25,7 +25,8 @@ OBJ = ROOT / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["attn_prep.hip", "attn_decode.hip", "attn_prefill.hip", "gemv.hip", "step.hip"]
+HIP_SOURCES = ["attn_prep.hip", "attn_decode.hip", "attn_prefill.hip", "gemv.hip", "step.hip",
+               "gdn.hip"]
 # Per-source code-generation flags. The prefill tile loop keeps 128 fp32 accumulators live; the
 # compiler's default MFMA register form parks them in AGPRs and copies all of them into VGPRs
 # on every iteration. The VGPR form keeps them in place.

@@ -1,5 +1,5 @@
-"""ctypes binding of the C ABI in include/qe_attn.h, include/qe_gemv.h and include/qe_step.h
-(libqe_attn.so), without the torch extension.
+"""ctypes binding of the C ABI in include/qe_attn.h, include/qe_gemv.h, include/qe_step.h and
+include/qe_gdn.h (libqe_attn.so), without the torch extension.
 
 This is the binding a non-torch host (or a test that must go through the C ABI) uses. Tensor
 arguments may be torch tensors (their data_ptr is passed) or raw integer device addresses.
@@ -49,6 +49,8 @@ SIGNATURES = {
     "qe_mtp_select": (_I, [_P, _P, _I, _P, _L, _P, _I, _P, _P, _P]),
     "qe_l2_persist_limit": (_I, [ctypes.c_size_t]),
     "qe_stream_access_window": (_I, [ctypes.c_size_t, ctypes.c_size_t, _F, _P]),
+    "qe_gdn_step_n": (_I, [_P, _P, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _I, _I,
+                           _I, _F, _P]),
 }
 
 HIP_SUCCESS = 0
@@ -154,3 +156,11 @@ def rmsnorm1p(x, delta, w, out, rows, H, ldx, ldd, ldo, eps, stream=None) -> int
 def argmax(x, rows, n, ldx, pv, pi, nb, out, idmap=None, stream=None) -> int:
     return load().qe_argmax(_ptr(x), rows, n, ldx, _ptr(pv), _ptr(pi), nb, _ptr(out), _ptr(idmap),
                             _stream(stream))
+
+
+def gdn_step_n(qkv, z, b, a, ldp, ring, conv_w, A_log, dt_bias, norm_w, S, st_k, st_v, st_g, ctl,
+               out, ldo, n, Hk, Hv, eps, stream=None) -> int:
+    return load().qe_gdn_step_n(_ptr(qkv), _ptr(z), _ptr(b), _ptr(a), ldp, _ptr(ring), _ptr(conv_w),
+                                _ptr(A_log), _ptr(dt_bias), _ptr(norm_w), _ptr(S), _ptr(st_k),
+                                _ptr(st_v), _ptr(st_g), _ptr(ctl), _ptr(out), ldo, n, Hk, Hv, eps,
+                                _stream(stream))

@@ -16,6 +16,7 @@
 #include <c10/hip/HIPStream.h>
 
 #include "qe_attn.h"
+#include "qe_gdn.h"
 #include "qe_gemv.h"
 #include "qe_step.h"
 
@@ -539,6 +540,70 @@ void mtp_select(torch::Tensor ctl, torch::Tensor mpos, int64_t off,
            "qe_mtp_select");
 }
 
+// ---- Gated DeltaNet step (reference csrc/bindings.cpp:118-145) -------------------------------
+// qkv / z / b / a are row views of one projection buffer sharing a row stride; S is
+// [Hv, 128, 128] fp32; the staging buffers hold 8 rows. `q` picks the reference's CUDA block
+// shape and is accepted for call compatibility only.
+struct GdnArgs {
+  int n, Hv;
+  long ldp, ldo;
+};
+GdnArgs parse_gdn(const torch::Tensor& qkv, const torch::Tensor& z, const torch::Tensor& b,
+                  const torch::Tensor& a, const torch::Tensor& ring, const torch::Tensor& conv_w,
+                  const torch::Tensor& A_log, const torch::Tensor& dt_bias,
+                  const torch::Tensor& norm_w, const torch::Tensor& S, const torch::Tensor& st_k,
+                  const torch::Tensor& st_v, const torch::Tensor& st_g, const torch::Tensor& ctl,
+                  const torch::Tensor& out, int64_t Hk, bool dev) {
+  const auto Q = rows(qkv, BF, "qkv", dev), Z = rows(z, BF, "z", dev), B = rows(b, BF, "b", dev),
+             A = rows(a, BF, "a", dev), O = rows(out, BF, "out", dev);
+  TORCH_CHECK(Q.ld == Z.ld && Q.ld == B.ld && Q.ld == A.ld, "qkv/z/b/a must share a row stride");
+  chk(ring, BF, "ring", dev);
+  chk(conv_w, BF, "conv_w", dev);
+  chk(A_log, BF, "A_log", dev);
+  chk(dt_bias, BF, "dt_bias", dev);
+  chk(norm_w, BF, "norm_w", dev);
+  chk(S, F32, "S", dev);
+  chk(st_k, F32, "st_k", dev);
+  chk(st_v, F32, "st_v", dev);
+  chk(st_g, F32, "st_g", dev);
+  chk(ctl, I32, "ctl", dev);
+  const int n = Q.n;
+  TORCH_CHECK(n >= 1 && n <= 8 && Z.n == n && B.n == n && A.n == n && O.n == n,
+              "gdn_step_n: 1..8 rows in every row argument");
+  TORCH_CHECK(S.dim() == 3 && S.size(1) == 128 && S.size(2) == 128, "dk = dv = 128 only");
+  const long Hv = S.size(0);
+  TORCH_CHECK(Hk >= 1 && Hv % Hk == 0, "Hv must be a multiple of Hk");
+  const long C = 2 * Hk * 128 + Hv * 128;
+  TORCH_CHECK(Q.w == C && ring.numel() == 16 * C && conv_w.numel() == 4 * C,
+              "qkv width, ring [16, C] and conv_w [C, 4] must match C = 2*Hk*128 + Hv*128");
+  TORCH_CHECK(Z.w == Hv * 128 && O.w == Hv * 128 && B.w == Hv && A.w == Hv,
+              "z and out are Hv*128 wide, b and a Hv wide");
+  TORCH_CHECK(A_log.numel() == Hv && dt_bias.numel() == Hv && norm_w.numel() == 128,
+              "A_log, dt_bias [Hv], norm_w [128]");
+  TORCH_CHECK(st_k.numel() == 8L * Hv * 128 && st_v.numel() == 8L * Hv * 128 &&
+                  st_g.numel() == 8L * Hv * 2,
+              "st_k, st_v [8, Hv, 128], st_g [8, Hv, 2]");
+  TORCH_CHECK(ctl.numel() >= 2, "ctl holds pos and pending");
+  return {n, (int)Hv, Q.ld, O.ld};
+}
+
+void gdn_step_n(torch::Tensor qkv, torch::Tensor z, torch::Tensor b, torch::Tensor a,
+                torch::Tensor ring, torch::Tensor conv_w, torch::Tensor A_log,
+                torch::Tensor dt_bias, torch::Tensor norm_w, torch::Tensor S, torch::Tensor st_k,
+                torch::Tensor st_v, torch::Tensor st_g, torch::Tensor ctl, torch::Tensor out,
+                int64_t Hk, double eps, int64_t q) {
+  (void)q;
+  const auto g = parse_gdn(qkv, z, b, a, ring, conv_w, A_log, dt_bias, norm_w, S, st_k, st_v,
+                           st_g, ctl, out, Hk, true);
+  const c10::DeviceGuard guard(S.device());
+  raise_on(qe_gdn_step_n(qkv.data_ptr(), z.data_ptr(), b.data_ptr(), a.data_ptr(), g.ldp,
+                         ring.data_ptr(), conv_w.data_ptr(), A_log.data_ptr(), dt_bias.data_ptr(),
+                         norm_w.data_ptr(), S.data_ptr<float>(), st_k.data_ptr<float>(),
+                         st_v.data_ptr<float>(), st_g.data_ptr<float>(), ctl.data_ptr<int>(),
+                         out.data_ptr(), g.ldo, g.n, (int)Hk, g.Hv, (float)eps, stream_of(S)),
+           "qe_gdn_step_n");
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "MI355X (gfx950) gated-attention decode ops with qengine._C's signatures";
   m.def("attn_prep", &attn_prep);
@@ -620,4 +685,26 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("_check_commit", [](torch::Tensor c, torch::Tensor t, torch::Tensor am, torch::Tensor d,
                             int64_t k) { parse_commit(c, t, am, d, k, false); });
   m.def("_check_gemv_bf16", &check_gemv_bf16, "validate gemv_bf16 arguments without launching");
+  m.def("gdn_step_n", &gdn_step_n, py::arg("qkv"), py::arg("z"), py::arg("b"), py::arg("a"),
+        py::arg("ring"), py::arg("conv_w"), py::arg("A_log"), py::arg("dt_bias"),
+        py::arg("norm_w"), py::arg("S"), py::arg("st_k"), py::arg("st_v"), py::arg("st_g"),
+        py::arg("ctl"), py::arg("out"), py::arg("Hk"), py::arg("eps"), py::arg("q") = 2,
+        "Gated DeltaNet step for n = 1..8 rows with lazy rollback (q: accepted, no effect)");
+  m.def("_check_gdn_step_n",
+        [](torch::Tensor qkv, torch::Tensor z, torch::Tensor b, torch::Tensor a, torch::Tensor ring,
+           torch::Tensor conv_w, torch::Tensor A_log, torch::Tensor dt_bias, torch::Tensor norm_w,
+           torch::Tensor S, torch::Tensor st_k, torch::Tensor st_v, torch::Tensor st_g,
+           torch::Tensor ctl, torch::Tensor out, int64_t Hk) {
+          const auto g = parse_gdn(qkv, z, b, a, ring, conv_w, A_log, dt_bias, norm_w, S, st_k,
+                                   st_v, st_g, ctl, out, Hk, false);
+          return std::vector<int64_t>{g.n, g.Hv, g.ldp, g.ldo};
+        },
+        py::arg("qkv"), py::arg("z"), py::arg("b"), py::arg("a"), py::arg("ring"),
+        py::arg("conv_w"), py::arg("A_log"), py::arg("dt_bias"), py::arg("norm_w"), py::arg("S"),
+        py::arg("st_k"), py::arg("st_v"), py::arg("st_g"), py::arg("ctl"), py::arg("out"),
+        py::arg("Hk"), "validate gdn_step_n arguments without launching");
+  m.def("set_gdn_phases", [](bool) {},
+        "no-op: the reference's phase-parallel A/B switch (one code path here)");
+  m.def("set_gdn_early", [](bool) {},
+        "no-op: the reference's overlap-with-producer A/B switch (no dependent launch on HIP)");
 }

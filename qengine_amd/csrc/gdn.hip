@@ -1,0 +1,288 @@
+// Gated DeltaNet decode / verify step on gfx950: n = 1..8 new rows per layer call with lazy
+// rollback (reference csrc/gdn.cu:1-25,65-311; math of python/qengine/reference.py:211-242).
+//
+// Per value head j (qk head i = j / (Hv/Hk)), with the committed fp32 state S_j [128][128] being
+// the state after position pos - pending:
+//   1. replay: the `pending` rows staged by the previous call (normalised k, v, decay, beta) are
+//      applied to S_j, which is written back once;
+//   2. new rows t < n at positions pos + t: causal conv (4 taps) + SiLU over the 384 channels of
+//      this head, gates, l2norm of q and k, the delta-rule update on a register copy of S_j, and
+//      the gated RMSNorm output; their (k, v, decay, beta) are staged for the next call, S_j is
+//      not advanced by them.
+// The same inline update runs for replayed and new rows, so the committed state after any
+// pattern of calls with kept prefixes equals plain one-row decoding bit for bit.
+//
+// gfx950 layout: one 512-thread workgroup (8 waves) per value head. Wave w owns state columns
+// 16w .. 16w+15; lane l holds rows 8(l>>2) .. +7 of columns 16w + 4(l&3) .. +3 (32 fp32 registers,
+// loaded as eight 16-byte rows). The dot products over the 128 state rows are a per-lane 8-term
+// FMA chain followed by a butterfly over the 16 lanes that share a column quad (DPP xor 8 / 4,
+// permlane16 / 32 swaps), so the recurrence needs no LDS and no barrier. Each wave therefore holds
+// the whole column: kv, delta and o never leave the wave. Three barriers per call: after the
+// per-call inputs are in LDS (staged rows, conv outputs, gates, l2 partial sums), after the
+// replay (by then q and k are normalised in LDS, once per channel), and before the gated
+// RMSNorm, which needs the 128 outputs of a row (wave t normalises row t).
+//
+// Conv history is a ring of 16 slots [16][C] keyed by absolute position (slot = pos & 15). A call
+// reads positions < pos from the ring (negative positions read as 0) and earlier rows of this
+// call from its own inputs, and writes the slots of positions pos .. pos+n-1. With n <= 8 the
+// read slots (pos-3 .. pos-1) and the written ones never alias, so workgroups sharing a qk head
+// need no synchronisation; only the workgroup with j % (Hv/Hk) == 0 writes the q/k channels.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "qe_device.hpp"
+#include "qe_gdn.h"
+
+namespace qe {
+
+constexpr int GDN_D = 128;      // dk = dv
+constexpr int GDN_RING = 16;
+constexpr int GDN_MAXN = 8;
+constexpr int GDN_THREADS = 512;
+
+struct __align__(16) F4 {
+  float x, y, z, w;
+};
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+// Sum over the 16 lanes that share lane & 3 (lane bits 2..5): xor 8 and xor 4 by DPP within a
+// 16-lane row, then xor 16 and xor 32 by the permlane swaps. Partners add the same two values,
+// so all 16 lanes get the same bits.
+__device__ __forceinline__ float colquad_sum(float v) {
+  v = v + dpp<0x128>(v);             // row_ror:8 = lane ^ 8
+  v = v + dpp<0x1B>(dpp<0x141>(v));  // row_half_mirror then quad_perm [3,2,1,0] = lane ^ 4
+  return group4_sum(v);              // lane ^ 16, lane ^ 32
+}
+
+// One delta-rule update of this lane's 8 x 4 block: S = decay S; kv = S^T k; delta = beta (v - kv);
+// S += k delta^T. The identical instruction sequence serves replayed and new rows.
+__device__ __forceinline__ void delta_step(float (&s)[8][4], const float (&k)[8], const float (&v)[4],
+                                           float decay, float beta) {
+  float kv[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      s[r][c] = s[r][c] * decay;
+      kv[c] = fmaf(s[r][c], k[r], kv[c]);
+    }
+  float delta[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) delta[c] = (v[c] - colquad_sum(kv[c])) * beta;
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s[r][c] = fmaf(k[r], delta[c], s[r][c]);
+}
+
+__device__ __forceinline__ void lds_read8(const float* p, float (&d)[8]) {
+  const F4 a = *reinterpret_cast<const F4*>(p), b = *reinterpret_cast<const F4*>(p + 4);
+  d[0] = a.x; d[1] = a.y; d[2] = a.z; d[3] = a.w; d[4] = b.x; d[5] = b.y; d[6] = b.z; d[7] = b.w;
+}
+__device__ __forceinline__ void lds_read4(const float* p, float (&d)[4]) {
+  const F4 a = *reinterpret_cast<const F4*>(p);
+  d[0] = a.x; d[1] = a.y; d[2] = a.z; d[3] = a.w;
+}
+
+__global__ void __launch_bounds__(GDN_THREADS)
+gdn_step_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
+                const __bf16* __restrict__ b, const __bf16* __restrict__ a, long ldp,
+                __bf16* __restrict__ ring, const __bf16* __restrict__ conv_w,
+                const __bf16* __restrict__ A_log, const __bf16* __restrict__ dt_bias,
+                const __bf16* __restrict__ norm_w, float* __restrict__ S,
+                float* __restrict__ st_k, float* __restrict__ st_v, float* __restrict__ st_g,
+                const int* __restrict__ ctl, __bf16* __restrict__ out, long ldo, int n, int Hk,
+                int Hv, float eps) {
+  __shared__ __align__(16) float sk[GDN_MAXN][GDN_D], sv[GDN_MAXN][GDN_D];  // replayed rows
+  __shared__ __align__(16) float qa[GDN_MAXN][GDN_D], ka[GDN_MAXN][GDN_D], va[GDN_MAXN][GDN_D];
+  __shared__ __align__(16) float oa[GDN_MAXN][GDN_D];
+  __shared__ float sg[GDN_MAXN][2], ga[GDN_MAXN][2], l2p[GDN_MAXN][4];
+
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int rg = lane >> 2, col0 = 16 * w + 4 * (lane & 3);
+  const int j = blockIdx.x, r = Hv / Hk, i = j / r;
+  const int C = 2 * Hk * GDN_D + Hv * GDN_D;
+  float* Sj = S + (size_t)j * GDN_D * GDN_D;
+
+  // Every global load below is unconditional with an in-bounds index (rows t >= n re-read row
+  // n - 1, unused staged rows are read anyway, history slots come from position & 15), so they
+  // issue back to back and the waits gather at their first uses; loads behind branches would
+  // each wait on their own. Order: the call's position, this call's inputs, the history and the
+  // staged rows, then the state block, which is needed last.
+  const int P = ctl[0];
+  const int pend = min(max(ctl[1], 0), GDN_MAXN);
+  const int part = tid >> 7, c = tid & 127;  // conv role (tid < 384): 0 = q, 1 = k, 2 = v
+  const int ch = part == 0 ? i * GDN_D + c : part == 1 ? (Hk + i) * GDN_D + c
+                                                        : 2 * Hk * GDN_D + j * GDN_D + c;
+  const int chl = tid < 3 * GDN_D ? ch : c;
+  const uint2 wv = *reinterpret_cast<const uint2*>(conv_w + (size_t)chl * 4);
+  __bf16 xb[GDN_MAXN];
+#pragma unroll
+  for (int t = 0; t < GDN_MAXN; ++t) xb[t] = qkv[(size_t)min(t, n - 1) * ldp + chl];
+  const int gt = tid - 3 * GDN_D;  // gate row of threads 384 .. 384+n-1
+  const int gtc = min(max(gt, 0), n - 1);
+  const __bf16 bb = b[(size_t)gtc * ldp + j], ab = a[(size_t)gtc * ldp + j];
+  const __bf16 dtb = dt_bias[j], alb = A_log[j];
+  const __bf16* zp = z + (size_t)min(w, n - 1) * ldp + j * GDN_D + 2 * lane;
+  const __bf16 zb0 = zp[0], zb1 = zp[1], nb0 = norm_w[2 * lane], nb1 = norm_w[2 * lane + 1];
+  __bf16 hb[3];  // x at positions P-3 .. P-1
+#pragma unroll
+  for (int q = 0; q < 3; ++q) hb[q] = ring[(size_t)((P - 3 + q) & (GDN_RING - 1)) * C + chl];
+  const int srow = tid >> 6, su = tid & 63;  // staged rows: thread = (row, 16-byte piece of k or v)
+  const F4 stv = *reinterpret_cast<const F4*>(
+      su < 32 ? st_k + ((size_t)srow * Hv + j) * GDN_D + 4 * su
+              : st_v + ((size_t)srow * Hv + j) * GDN_D + 4 * (su - 32));
+  const float2 stg = *reinterpret_cast<const float2*>(st_g + ((size_t)(tid & 7) * Hv + j) * 2);
+  float s[8][4];
+#pragma unroll
+  for (int rr = 0; rr < 8; ++rr) {
+    const F4 v = *reinterpret_cast<const F4*>(Sj + (size_t)(rg * 8 + rr) * GDN_D + col0);
+    s[rr][0] = v.x; s[rr][1] = v.y; s[rr][2] = v.z; s[rr][3] = v.w;
+  }
+
+  *reinterpret_cast<F4*>(su < 32 ? &sk[srow][4 * su] : &sv[srow][4 * (su - 32)]) = stv;
+  if (tid < GDN_MAXN) {
+    sg[tid][0] = stg.x;
+    sg[tid][1] = stg.y;
+  }
+  const float z0 = bf16_to_f32(zb0), z1 = bf16_to_f32(zb1);
+  const float nw0 = bf16_to_f32(nb0), nw1 = bf16_to_f32(nb1);
+  if (tid < 3 * GDN_D) {
+    const float cw[4] = {lo_bf16(wv.x), hi_bf16(wv.x), lo_bf16(wv.y), hi_bf16(wv.y)};
+    // x at positions P-3 .. P+n-1: history from the ring (zero before the sequence), then this
+    // call's rows
+    float xs[3 + GDN_MAXN];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) xs[q] = P - 3 + q >= 0 ? bf16_to_f32(hb[q]) : 0.f;
+#pragma unroll
+    for (int t = 0; t < GDN_MAXN; ++t) xs[3 + t] = bf16_to_f32(xb[t]);
+    const bool writes_ring = part == 2 || j % r == 0;  // q/k channels are shared by r heads
+#pragma unroll
+    for (int t = 0; t < GDN_MAXN; ++t) {
+      if (t < n) {
+        float acc = cw[0] * xs[t];  // buffer order [x_{t-3}, x_{t-2}, x_{t-1}, x_t]
+        acc = fmaf(cw[1], xs[t + 1], acc);
+        acc = fmaf(cw[2], xs[t + 2], acc);
+        acc = fmaf(cw[3], xs[t + 3], acc);
+        const float y = round_bf16(silu_f(round_bf16(acc)));
+        if (part == 0) qa[t][c] = y;
+        else if (part == 1) ka[t][c] = y;
+        else va[t][c] = y;
+        if (writes_ring) ring[(size_t)((P + t) & (GDN_RING - 1)) * C + ch] = xb[t];
+        if (part < 2) {  // sum of squares of q (waves 0, 1) and k (waves 2, 3)
+          const float ss = wave_sum_fast(y * y);
+          if (lane == 0) l2p[t][w] = ss;
+        }
+      }
+    }
+  }
+  if (gt >= 0 && gt < n) {
+    const float beta = round_bf16(sigmoid_f32(bf16_to_f32(bb)));
+    const float x = bf16_to_f32(ab) + bf16_to_f32(dtb);
+    const float sp = x > 20.f ? x : log1pf(expf(x));  // softplus, threshold 20
+    const float decay = expf(-expf(bf16_to_f32(alb)) * sp);
+    ga[gt][0] = decay;
+    ga[gt][1] = beta;
+  }
+  __syncthreads();
+
+  // Stage this call's v and gates for the next call's replay. Only after the barrier: the staged
+  // rows of the previous call (same addresses) have all been read into LDS by then.
+  for (int t = tid >> 7; t < n; t += GDN_THREADS / GDN_D)
+    st_v[((size_t)t * Hv + j) * GDN_D + c] = va[t][c];
+  if (tid < n)
+    *reinterpret_cast<float2*>(st_g + ((size_t)tid * Hv + j) * 2) = make_float2(ga[tid][0], ga[tid][1]);
+
+  // Normalise this call's q and k once per channel (threads 0-255 own one q or k channel each)
+  // and stage k for the next call. In place: the rows are read again only after the barrier
+  // that follows the replay.
+  if (tid < 2 * GDN_D) {
+    const float sqrt_dk = 11.313708498984761f;  // sqrt(128) rounded to fp32
+    for (int t = 0; t < n; ++t) {
+      const float ss = tid < GDN_D ? l2p[t][0] + l2p[t][1] : l2p[t][2] + l2p[t][3];
+      const float inv = 1.0f / sqrtf(ss + 1e-6f);
+      if (tid < GDN_D) {
+        qa[t][c] = (qa[t][c] * inv) / sqrt_dk;
+      } else {
+        const float kn = ka[t][c] * inv;
+        ka[t][c] = kn;
+        st_k[((size_t)t * Hv + j) * GDN_D + c] = kn;
+      }
+    }
+  }
+
+  // ---- 1. replay the rows kept by the previous call, write the committed state back ----
+  for (int t = 0; t < pend; ++t) {
+    float k[8], v[4];
+    lds_read8(&sk[t][rg * 8], k);
+    lds_read4(&sv[t][col0], v);
+    delta_step(s, k, v, sg[t][0], sg[t][1]);
+  }
+  if (pend > 0) {
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr)
+      *reinterpret_cast<F4*>(Sj + (size_t)(rg * 8 + rr) * GDN_D + col0) =
+          F4{s[rr][0], s[rr][1], s[rr][2], s[rr][3]};
+  }
+  __syncthreads();
+
+  // ---- 2. new rows on the register copy ----
+  for (int t = 0; t < n; ++t) {
+    float k[8], q[8], v[4];
+    lds_read8(&ka[t][rg * 8], k);
+    lds_read8(&qa[t][rg * 8], q);
+    lds_read4(&va[t][col0], v);
+    delta_step(s, k, v, ga[t][0], ga[t][1]);
+    float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr)
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) o[cc] = fmaf(s[rr][cc], q[rr], o[cc]);
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) o[cc] = round_bf16(colquad_sum(o[cc]));
+    if (rg == 0) *reinterpret_cast<F4*>(&oa[t][col0]) = F4{o[0], o[1], o[2], o[3]};
+  }
+  __syncthreads();
+
+  // ---- gated RMSNorm: wave t normalises row t ----
+  if (w < n) {
+    const float2 o = *reinterpret_cast<const float2*>(&oa[w][2 * lane]);
+    const float ss = wave_sum_fast(o.x * o.x + o.y * o.y);
+    const float inv = 1.0f / sqrtf(ss / 128.0f + eps);
+    const float y0 = round_bf16(nw0 * round_bf16(o.x * inv));  // bf16 weight * bf16 norm
+    const float y1 = round_bf16(nw1 * round_bf16(o.y * inv));
+    __bf16* op = out + (size_t)w * ldo + j * GDN_D + 2 * lane;
+    op[0] = f32_to_bf16(y0 * silu_f(z0));
+    op[1] = f32_to_bf16(y1 * silu_f(z1));
+  }
+}
+
+}  // namespace qe
+
+using namespace qe;
+
+extern "C" hipError_t qe_gdn_step_n(const void* qkv, const void* z, const void* b, const void* a,
+                                    long ldp, void* ring, const void* conv_w, const void* A_log,
+                                    const void* dt_bias, const void* norm_w, float* S, float* st_k,
+                                    float* st_v, float* st_g, const int* ctl, void* out, long ldo,
+                                    int n, int Hk, int Hv, float eps, hipStream_t stream) {
+  auto al = [](const void* p, uintptr_t m) { return (reinterpret_cast<uintptr_t>(p) & (m - 1)) == 0; };
+  if (!qkv || !z || !b || !a || !ring || !conv_w || !A_log || !dt_bias || !norm_w || !S || !st_k ||
+      !st_v || !st_g || !ctl || !out)
+    return hipErrorInvalidValue;
+  if (n < 1 || n > GDN_MAXN || Hk < 1 || Hv < 1 || Hv % Hk != 0 || Hv > 65535)
+    return hipErrorInvalidValue;
+  const long C = 2L * Hk * GDN_D + (long)Hv * GDN_D;
+  if (C >= (1L << 26) || ldp < C || ldo < (long)Hv * GDN_D) return hipErrorInvalidValue;
+  if (!al(S, 16) || !al(st_k, 16) || !al(st_v, 16) || !al(st_g, 8) || !al(conv_w, 8))
+    return hipErrorInvalidValue;
+  gdn_step_kernel<<<dim3(Hv), dim3(GDN_THREADS), 0, stream>>>(
+      static_cast<const __bf16*>(qkv), static_cast<const __bf16*>(z), static_cast<const __bf16*>(b),
+      static_cast<const __bf16*>(a), ldp, static_cast<__bf16*>(ring),
+      static_cast<const __bf16*>(conv_w), static_cast<const __bf16*>(A_log),
+      static_cast<const __bf16*>(dt_bias), static_cast<const __bf16*>(norm_w), S, st_k, st_v, st_g,
+      ctl, static_cast<__bf16*>(out), ldo, n, Hk, Hv, eps);
+  return hipGetLastError();
+}

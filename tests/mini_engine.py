@@ -2,7 +2,9 @@
 engine drives qengine._C (python/qengine/engine.py:384-520): per-layer rmsnorm1p with the fused
 residual, in_proj GEMV, attn_prep, attn_decode, o_proj GEMV, SwiGLU MLP, final norm, lm_head
 GEMV, argmax, accept and commit, all on device buffers, one hipGraph per pass width. Weights are
-random (there is no checkpoint here) and every layer is a gated-attention layer.
+random (there is no checkpoint here). Layers are gated-attention layers, or Gated DeltaNet layers
+(in_proj GEMV, gdn_step_n with its lazy rollback, out_proj GEMV) where ``layer_types`` says
+"linear_attention", as in the reference's hybrid model (engine.py:436-448).
 
 Test infrastructure: it exists to check that a whole step runs as one graph and that
 speculative verify passes reproduce plain greedy decoding token for token.
@@ -20,8 +22,11 @@ HD = 256
 
 class MiniEngine:
     def __init__(self, layers=2, hidden=1024, inter=2048, vocab=4096, hq=24, hkv=4, max_len=256,
-                 seed=0, device="cuda"):
+                 seed=0, device="cuda", layer_types=None, hk=4, hv=8):
         self.dev, self.H, self.I, self.V, self.hq, self.hkv = device, hidden, inter, vocab, hq, hkv
+        self.types = list(layer_types or ["full_attention"] * layers)
+        assert len(self.types) == layers
+        self.hk, self.hv = hk, hv
         self.max_len, self.eps = max_len, 1e-6
         g = torch.Generator(device=device).manual_seed(seed)
 
@@ -33,14 +38,31 @@ class MiniEngine:
 
         H, I = hidden, inter
         self.attn_n = hq * 2 * HD + 2 * hkv * HD
+        self.conv_dim = 2 * hk * 128 + hv * 128
+        self.gdn_n = self.conv_dim + hv * 128 + 2 * hv
         self.embed_t = (torch.randn(vocab, H, device=device, generator=g)).to(BF)
         self.layers = []
-        for _ in range(layers):
-            self.layers.append(dict(
-                in_norm=norm_w(H), post_norm=norm_w(H), q_norm=norm_w(HD), k_norm=norm_w(HD),
-                in_proj=w(self.attn_n, H), out=w(H, hq * HD), gate_up=w(2 * I, H), down=w(H, I),
-                kc=torch.zeros(hkv, max_len, HD, dtype=BF, device=device),
-                vc=torch.zeros(hkv, max_len, HD, dtype=BF, device=device)))
+        for t in self.types:
+            L = dict(type=t, in_norm=norm_w(H), post_norm=norm_w(H), gate_up=w(2 * I, H),
+                     down=w(H, I))
+            if t == "linear_attention":
+                L.update(
+                    in_proj=w(self.gdn_n, H), out=w(H, hv * 128),
+                    conv_w=(torch.randn(self.conv_dim, 1, 4, device=device, generator=g) * 0.5).to(BF),
+                    A_log=(torch.rand(hv, device=device, generator=g) * 2 - 1).to(BF),
+                    dt_bias=torch.randn(hv, device=device, generator=g).to(BF),
+                    norm_w=(1 + 0.1 * torch.randn(128, device=device, generator=g)).to(BF),
+                    ring=torch.zeros(16, self.conv_dim, dtype=BF, device=device),
+                    S=torch.zeros(hv, 128, 128, device=device),
+                    st=[torch.zeros(NMAX, hv, 128, device=device),
+                        torch.zeros(NMAX, hv, 128, device=device),
+                        torch.zeros(NMAX, hv, 2, device=device)])
+            else:
+                L.update(q_norm=norm_w(HD), k_norm=norm_w(HD), in_proj=w(self.attn_n, H),
+                         out=w(H, hq * HD),
+                         kc=torch.zeros(hkv, max_len, HD, dtype=BF, device=device),
+                         vc=torch.zeros(hkv, max_len, HD, dtype=BF, device=device))
+            self.layers.append(L)
         self.final_norm = norm_w(H)
         self.lm_head = w(vocab, H, scale=4.0)
         z = lambda *s, dt=BF: torch.zeros(*s, dtype=dt, device=device)  # noqa: E731
@@ -49,8 +71,8 @@ class MiniEngine:
         self.am, self.next_tok, self.drafts = z(NMAX, dt=I32), z(NMAX, dt=I32), z(NMAX, dt=I32)
         self.log = z(max_len, dt=I32)
         self.h, self.xn, self.mo, self.hid = z(NMAX, H), z(NMAX, H), z(NMAX, H), z(NMAX, H)
-        self.proj = z(NMAX, (self.attn_n + 7) // 8 * 8)
-        self.mix = z(NMAX, hq * HD)
+        self.proj = z(NMAX, (max(self.attn_n, self.gdn_n) + 7) // 8 * 8)
+        self.mix = z(NMAX, max(hq * HD, hv * 128))
         self.gu, self.act = z(NMAX, 2 * I), z(NMAX, I)
         self.logits = z(NMAX, vocab)
         self.am_v, self.am_i = z(NMAX * 256, dt=F32), z(NMAX * 256, dt=I32)
@@ -63,20 +85,33 @@ class MiniEngine:
     def reset(self):
         self.ctl.zero_()
         self.log.zero_()
+        for L in self.layers:
+            if L["type"] == "linear_attention":
+                L["ring"].zero_()
+                L["S"].zero_()
 
     # ------------------------------------------------------------------ one pass of n rows
     def _layer(self, L, n, first):
         C, h, xn, mo = qa._C, self.h[:n], self.xn[:n], self.mo[:n]
         C.rmsnorm1p(h, None if first else mo, L["in_norm"], xn, self.eps)
-        pr = self.proj[:n, :self.attn_n]
-        C.gemv_bf16(L["in_proj"], xn, pr)
-        q0 = self.hq * 2 * HD
-        k1 = q0 + self.hkv * HD
-        qg, q = pr[:, :q0], self.q[:n]
-        C.attn_prep(qg, pr[:, q0:k1], pr[:, k1:], L["q_norm"], L["k_norm"], self.inv_freq,
-                    self.ctl, q, L["kc"], L["vc"], self.eps)
-        out = self.mix[:n]
-        C.attn_decode(q, L["kc"], L["vc"], self.ctl, qg, self.part_o, self.part_ml, out)
+        if L["type"] == "linear_attention":
+            pr = self.proj[:n, :self.gdn_n]
+            C.gemv_bf16(L["in_proj"], xn, pr)
+            c0, c1, hv = self.conv_dim, self.conv_dim + self.hv * 128, self.hv
+            out = self.mix[:n, :hv * 128]
+            C.gdn_step_n(pr[:, :c0], pr[:, c0:c1], pr[:, c1:c1 + hv], pr[:, c1 + hv:], L["ring"],
+                         L["conv_w"], L["A_log"], L["dt_bias"], L["norm_w"], L["S"], *L["st"],
+                         self.ctl, out, self.hk, self.eps)
+        else:
+            pr = self.proj[:n, :self.attn_n]
+            C.gemv_bf16(L["in_proj"], xn, pr)
+            q0 = self.hq * 2 * HD
+            k1 = q0 + self.hkv * HD
+            qg, q = pr[:, :q0], self.q[:n]
+            C.attn_prep(qg, pr[:, q0:k1], pr[:, k1:], L["q_norm"], L["k_norm"], self.inv_freq,
+                        self.ctl, q, L["kc"], L["vc"], self.eps)
+            out = self.mix[:n, :self.hq * HD]
+            C.attn_decode(q, L["kc"], L["vc"], self.ctl, qg, self.part_o, self.part_ml, out)
         C.gemv_bf16(L["out"], out, mo)
         C.rmsnorm1p(h, mo, L["post_norm"], xn, self.eps)
         C.gemv_bf16(L["gate_up"], xn, self.gu[:n])
@@ -94,17 +129,26 @@ class MiniEngine:
         C.accept(self.in_tok, self.am, n, self.ctl, self.next_tok, self.log)
         C.commit(self.ctl, self.in_tok, self.am, self.drafts, k)
 
+    def _mutable(self):
+        """Device state a pass changes: bookkeeping, and the recurrent layers' ring, state and
+        staged rows (a pass replays staged rows into S, so a warm-up pass must be undone)."""
+        out = [self.ctl, self.in_tok, self.log]
+        for L in self.layers:
+            if L["type"] == "linear_attention":
+                out += [L["ring"], L["S"], *L["st"]]
+        return out
+
     def graph(self, n, k):
         """The whole pass of n rows (k drafts staged for the next one) as one hipGraph."""
         if (n, k) not in self.graphs:
-            saved = [t.clone() for t in (self.ctl, self.in_tok, self.log)]
+            saved = [t.clone() for t in self._mutable()]
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(side):
                 self._pass(n, k)  # warm-up outside capture (its state changes are undone below)
             torch.cuda.current_stream().wait_stream(side)
             torch.cuda.synchronize()
-            for t, s in zip((self.ctl, self.in_tok, self.log), saved):
+            for t, s in zip(self._mutable(), saved):
                 t.copy_(s)
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):

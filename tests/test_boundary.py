@@ -382,3 +382,70 @@ def test_step_ops_contract(native):
     C._check_commit(ints(24), ints(8), ints(8), ints(7), 7)
     with pytest.raises(RuntimeError, match="commit"):
         C._check_commit(ints(24), ints(7), ints(8), ints(7), 7)
+
+
+# ------------------------------------------------------------------ Gated DeltaNet step (gdn.cu)
+def _gdn_args(**kw):
+    """qe_gdn_step_n arguments for hk=16, hv=48 (C = 10240) with fake but aligned pointers."""
+    a = dict(qkv=A, z=A, b=A, a=A, ldp=16504, ring=A, conv_w=A, A_log=A, dt_bias=A, norm_w=A,
+             S=A, st_k=A, st_v=A, st_g=A, ctl=A, out=A, ldo=6144, n=1, Hk=16, Hv=48, eps=1e-6,
+             stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("kw,why", [
+    (dict(n=0), "no rows"), (dict(n=9), "more than 8 rows"), (dict(Hv=40), "Hv % Hk != 0"),
+    (dict(Hk=0), "no qk heads"), (dict(ldp=10000), "ldp < C"), (dict(ldo=6000), "ldo < Hv*128"),
+    (dict(S=A + 4), "S not 16-byte aligned"), (dict(st_g=A + 4), "st_g not 8-byte aligned"),
+    (dict(conv_w=A + 2), "conv_w not 8-byte aligned"), (dict(ctl=None), "null ctl"),
+    (dict(Hk=1, Hv=65536, ldp=1 << 40, ldo=1 << 40), "more value heads than grid blocks"),
+])
+def test_capi_gdn_rejects(capi, kw, why):
+    assert capi.load().qe_gdn_step_n(*_gdn_args(**kw)) == INVALID, why
+
+
+def _gdn_tensors(hk=16, hv=48, n=3, pad=24):
+    Cd = 2 * hk * 128 + hv * 128
+    w = Cd + hv * 128 + 2 * hv
+    pr = torch.zeros(n, w + pad, dtype=BF)
+    c1 = Cd + hv * 128
+    return dict(qkv=pr[:, :Cd], z=pr[:, Cd:c1], b=pr[:, c1:c1 + hv], a=pr[:, c1 + hv:w],
+                ring=torch.zeros(16, Cd, dtype=BF), conv_w=torch.zeros(Cd, 1, 4, dtype=BF),
+                A_log=torch.zeros(hv, dtype=BF), dt_bias=torch.zeros(hv, dtype=BF),
+                norm_w=torch.zeros(128, dtype=BF), S=torch.zeros(hv, 128, 128),
+                st_k=torch.zeros(8, hv, 128), st_v=torch.zeros(8, hv, 128),
+                st_g=torch.zeros(8, hv, 2), ctl=torch.zeros(8, dtype=I32),
+                out=torch.zeros(n, hv * 128, dtype=BF), Hk=hk)
+
+
+def test_gdn_contract(native):
+    """The reference's checks for gdn_step_n (csrc/bindings.cpp:118-145) without a GPU."""
+    C = native
+    t = _gdn_tensors()
+    assert list(C._check_gdn_step_n(**t)) == [3, 48, t["qkv"].stride(0), 6144]
+
+    def bad(msg, **kw):
+        u = dict(t)
+        u.update(kw)
+        with pytest.raises(RuntimeError, match=msg):
+            C._check_gdn_step_n(**u)
+
+    bad("share a row stride", z=torch.zeros(3, 6144, dtype=BF))
+    bad("1..8 rows", out=torch.zeros(2, 6144, dtype=BF))
+    t9 = _gdn_tensors(n=9)
+    with pytest.raises(RuntimeError, match="1..8 rows"):
+        C._check_gdn_step_n(**t9)
+    bad("dk = dv = 128", S=torch.zeros(48, 64, 128))
+    bad("multiple of Hk", Hk=5)
+    bad("ring", ring=torch.zeros(15, 10240, dtype=BF))
+    bad("conv_w", conv_w=torch.zeros(10240, 3, dtype=BF))
+    bad("Hv\\*128 wide", out=torch.zeros(3, 6000, dtype=BF))
+    bad("A_log", norm_w=torch.zeros(64, dtype=BF))
+    bad("st_k", st_g=torch.zeros(8, 48, 1))
+    bad("wrong dtype", S=torch.zeros(48, 128, 128, dtype=torch.float64))
+    bad("ctl", ctl=torch.zeros(1, dtype=I32))
+    with pytest.raises(RuntimeError, match="device"):
+        C.gdn_step_n(**t, eps=1e-6)
+    C.set_gdn_phases(True)
+    C.set_gdn_early(True)

@@ -2,7 +2,9 @@
 final norm, lm_head, argmax, accept, commit) replayed as one hipGraph, and speculative verify
 passes producing exactly the tokens of plain greedy decoding, whatever the drafts (the invariant
 of the reference's tests/test_spec.py:57-67 and README.md:30-31). It holds because every op
-computes row r of an n-row pass bit-identically to a 1-row pass."""
+computes row r of an n-row pass bit-identically to a 1-row pass. The hybrid engine adds Gated
+DeltaNet layers, whose lazy rollback (staged rows replayed by the next pass) must give the same
+tokens and, once replayed, the same recurrent state as plain decoding."""
 import pytest
 import torch
 
@@ -63,3 +65,52 @@ def test_plain_graph_replays_match_eager_passes(engine, plain):
     torch.cuda.synchronize()
     P = len(PROMPT)
     assert engine.log[P: P + N_NEW].tolist() == plain
+
+
+# ---------------------------------------------------------------- hybrid: Gated DeltaNet + attention
+HYBRID = ["linear_attention", "linear_attention", "full_attention", "linear_attention"]
+
+
+@pytest.fixture(scope="module")
+def hybrid(native):
+    """The reference model's layer pattern (three recurrent layers to one attention layer),
+    small: the recurrent layers' lazy rollback is exercised inside the step graph."""
+    return MiniEngine(layers=4, hidden=1024, inter=2048, vocab=4096, max_len=128, seed=5,
+                      layer_types=HYBRID, hk=4, hv=8)
+
+
+@pytest.fixture(scope="module")
+def hybrid_plain(hybrid):
+    toks = hybrid.generate_plain(PROMPT, N_NEW)
+    assert len(set(toks)) > 3, toks
+    return toks
+
+
+@pytest.mark.parametrize("kind", ["right", "wrong", "mixed"])
+def test_hybrid_spec_equals_plain(hybrid, hybrid_plain, kind):
+    toks, passes, ctl = hybrid.generate_spec(PROMPT, N_NEW, _drafter(hybrid_plain, kind), k=3)
+    assert toks == hybrid_plain
+    if kind == "wrong":
+        assert ctl[5] == 0 and passes == N_NEW - 1
+    if kind == "mixed":
+        assert 0 < ctl[5] < 3 * passes
+
+
+def test_hybrid_state_after_spec_equals_plain(hybrid, hybrid_plain):
+    """After the same tokens, speculative and plain decoding leave the same recurrent state once
+    the pending rows are replayed (one more 1-row pass each), bit for bit."""
+    P = len(PROMPT)
+    hybrid.generate_spec(PROMPT, N_NEW, _drafter(hybrid_plain, "mixed"), k=3)
+    stop = int(hybrid.ctl[0])
+    states = []
+    for mode in ("spec", "plain"):
+        if mode == "plain":  # plain decoding to the same position
+            hybrid.generate_plain(PROMPT, stop - P + 1)
+        assert int(hybrid.ctl[0]) == stop
+        hybrid.in_tok[0] = 7
+        hybrid._pass(1, 0)  # replays every pending row into S
+        torch.cuda.synchronize()
+        states.append([L["S"].clone() for L in hybrid.layers if L["type"] == "linear_attention"])
+        if mode == "spec":
+            hybrid.reset()
+    assert all(torch.equal(a, b) for a, b in zip(*states))
