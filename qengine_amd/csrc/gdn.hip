@@ -12,6 +12,10 @@
 // The same inline update runs for replayed and new rows, so the committed state after any
 // pattern of calls with kept prefixes equals plain one-row decoding bit for bit.
 //
+// Two kernels share the per-column arithmetic and so give the same bits: gdn_step_kernel (one
+// workgroup per head, below) for 1-row calls and large Hv, and gdn_split_kernel (each head over
+// 4 workgroups, further down) for 2-8 rows when its grid fits the GPU at once.
+//
 // gfx950 layout: one 512-thread workgroup (8 waves) per value head. Wave w owns state columns
 // 16w .. 16w+15; lane l holds rows 8(l>>2) .. +7 of columns 16w + 4(l&3) .. +3 (32 fp32 registers,
 // loaded as eight 16-byte rows). The dot products over the 128 state rows are a per-lane 8-term
@@ -40,6 +44,11 @@ constexpr int GDN_D = 128;      // dk = dv
 constexpr int GDN_RING = 16;
 constexpr int GDN_MAXN = 8;
 constexpr int GDN_THREADS = 512;
+constexpr int GDN_SPLIT = 4;                        // workgroups per head in the split kernel
+constexpr int GDN_SPLIT_COLS = GDN_D / GDN_SPLIT;
+constexpr int GDN_SPLIT_THREADS = 512;
+constexpr int GDN_SPLIT_MAX_HV = 64;                // exchange table size (heads)
+constexpr int GDN_SPIN_LIMIT = 1 << 18;
 
 struct __align__(16) F4 {
   float x, y, z, w;
@@ -56,25 +65,63 @@ __device__ __forceinline__ float colquad_sum(float v) {
   return group4_sum(v);              // lane ^ 16, lane ^ 32
 }
 
-// One delta-rule update of this lane's 8 x 4 block: S = decay S; kv = S^T k; delta = beta (v - kv);
-// S += k delta^T. The identical instruction sequence serves replayed and new rows.
-__device__ __forceinline__ void delta_step(float (&s)[8][4], const float (&k)[8], const float (&v)[4],
-                                           float decay, float beta) {
-  float kv[4] = {0.f, 0.f, 0.f, 0.f};
+// One delta-rule update of this lane's 8 x NC block: S = decay S; kv = S^T k; delta =
+// beta (v - kv); S += k delta^T. The identical instruction sequence serves replayed and new rows,
+// and each column's arithmetic (an 8-term chain over rows 8 rg .. +7, then the 16-lane
+// butterfly) does not depend on NC, so both kernels below compute the same state bits.
+template <int NC>
+__device__ __forceinline__ void delta_step(float (&s)[8][NC], const float (&k)[8],
+                                           const float (&v)[NC], float decay, float beta) {
+  float kv[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) kv[c] = 0.f;
 #pragma unroll
   for (int r = 0; r < 8; ++r)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < NC; ++c) {
       s[r][c] = s[r][c] * decay;
       kv[c] = fmaf(s[r][c], k[r], kv[c]);
     }
-  float delta[4];
+  float delta[NC];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) delta[c] = (v[c] - colquad_sum(kv[c])) * beta;
+  for (int c = 0; c < NC; ++c) delta[c] = (v[c] - colquad_sum(kv[c])) * beta;
 #pragma unroll
   for (int r = 0; r < 8; ++r)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) s[r][c] = fmaf(k[r], delta[c], s[r][c]);
+    for (int c = 0; c < NC; ++c) s[r][c] = fmaf(k[r], delta[c], s[r][c]);
+}
+
+// o = S^T q for this lane's columns, rounded to bf16 (the reference casts core_attn_out).
+template <int NC>
+__device__ __forceinline__ void read_out(const float (&s)[8][NC], const float (&q)[8],
+                                         float (&o)[NC]) {
+#pragma unroll
+  for (int c = 0; c < NC; ++c) o[c] = 0.f;
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) o[c] = fmaf(s[r][c], q[r], o[c]);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) o[c] = round_bf16(colquad_sum(o[c]));
+}
+
+// Causal conv (4 taps, the HF buffer order [x_{t-3}, x_{t-2}, x_{t-1}, x_t]) and SiLU of row t of
+// one channel; xs holds x at positions P-3 .. P+n-1. Rounds to bf16 after the conv and after SiLU.
+__device__ __forceinline__ float conv_silu(const float (&cw)[4], const float (&xs)[3 + GDN_MAXN],
+                                           int t) {
+  float acc = cw[0] * xs[t];
+  acc = fmaf(cw[1], xs[t + 1], acc);
+  acc = fmaf(cw[2], xs[t + 2], acc);
+  acc = fmaf(cw[3], xs[t + 3], acc);
+  return round_bf16(silu_f(round_bf16(acc)));
+}
+
+// beta = bf16(sigmoid(b)); decay = exp(-exp(A_log) * softplus(a + dt_bias)), threshold 20.
+__device__ __forceinline__ float2 gate_values(__bf16 bb, __bf16 ab, __bf16 dtb, __bf16 alb) {
+  const float beta = round_bf16(sigmoid_f32(bf16_to_f32(bb)));
+  const float x = bf16_to_f32(ab) + bf16_to_f32(dtb);
+  const float sp = x > 20.f ? x : log1pf(expf(x));
+  return make_float2(expf(-expf(bf16_to_f32(alb)) * sp), beta);
 }
 
 __device__ __forceinline__ void lds_read8(const float* p, float (&d)[8]) {
@@ -162,11 +209,7 @@ gdn_step_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
 #pragma unroll
     for (int t = 0; t < GDN_MAXN; ++t) {
       if (t < n) {
-        float acc = cw[0] * xs[t];  // buffer order [x_{t-3}, x_{t-2}, x_{t-1}, x_t]
-        acc = fmaf(cw[1], xs[t + 1], acc);
-        acc = fmaf(cw[2], xs[t + 2], acc);
-        acc = fmaf(cw[3], xs[t + 3], acc);
-        const float y = round_bf16(silu_f(round_bf16(acc)));
+        const float y = conv_silu(cw, xs, t);
         if (part == 0) qa[t][c] = y;
         else if (part == 1) ka[t][c] = y;
         else va[t][c] = y;
@@ -179,12 +222,9 @@ gdn_step_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
     }
   }
   if (gt >= 0 && gt < n) {
-    const float beta = round_bf16(sigmoid_f32(bf16_to_f32(bb)));
-    const float x = bf16_to_f32(ab) + bf16_to_f32(dtb);
-    const float sp = x > 20.f ? x : log1pf(expf(x));  // softplus, threshold 20
-    const float decay = expf(-expf(bf16_to_f32(alb)) * sp);
-    ga[gt][0] = decay;
-    ga[gt][1] = beta;
+    const float2 gv = gate_values(bb, ab, dtb, alb);
+    ga[gt][0] = gv.x;
+    ga[gt][1] = gv.y;
   }
   __syncthreads();
 
@@ -235,13 +275,8 @@ gdn_step_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
     lds_read8(&qa[t][rg * 8], q);
     lds_read4(&va[t][col0], v);
     delta_step(s, k, v, ga[t][0], ga[t][1]);
-    float o[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int rr = 0; rr < 8; ++rr)
-#pragma unroll
-      for (int cc = 0; cc < 4; ++cc) o[cc] = fmaf(s[rr][cc], q[rr], o[cc]);
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) o[cc] = round_bf16(colquad_sum(o[cc]));
+    float o[4];
+    read_out(s, q, o);
     if (rg == 0) *reinterpret_cast<F4*>(&oa[t][col0]) = F4{o[0], o[1], o[2], o[3]};
   }
   __syncthreads();
@@ -249,7 +284,19 @@ gdn_step_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
   // ---- gated RMSNorm: wave t normalises row t ----
   if (w < n) {
     const float2 o = *reinterpret_cast<const float2*>(&oa[w][2 * lane]);
-    const float ss = wave_sum_fast(o.x * o.x + o.y * o.y);
+    // Sum of squares in the split kernel's order (four serial 32-column partials, added in
+    // order), so both kernels give the same bits and a call may use either.
+    float part_ss = 0.f;
+    if (lane < GDN_SPLIT) {
+#pragma unroll
+      for (int cc = 0; cc < GDN_D / GDN_SPLIT; ++cc)
+        part_ss = fmaf(oa[w][lane * (GDN_D / GDN_SPLIT) + cc], oa[w][lane * (GDN_D / GDN_SPLIT) + cc],
+                       part_ss);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int g = 0; g < GDN_SPLIT; ++g)
+      ss += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part_ss), g));
     const float inv = 1.0f / sqrtf(ss / 128.0f + eps);
     const float y0 = round_bf16(nw0 * round_bf16(o.x * inv));  // bf16 weight * bf16 norm
     const float y1 = round_bf16(nw1 * round_bf16(o.y * inv));
@@ -259,9 +306,272 @@ gdn_step_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
   }
 }
 
+// ------------------------------------------------------------------ split kernel
+// The same step with each head's 128 state columns split over GDN_SPLIT workgroups of 256
+// threads (32 columns each): four times the CUs for the state I/O and the delta-rule VALU work,
+// which bound the one-workgroup kernel. Each workgroup holds rows 8 rg .. +7 of two columns per
+// lane (wave w: local columns 8w .. 8w+7) and runs the same per-column arithmetic, so the state
+// is bit-identical to the one-workgroup kernel's. Every workgroup repeats the conv, l2norm and
+// gates of its head's q and k (256 channels) and does the v channels of its own columns.
+//
+// The gated RMSNorm needs the sum of squares of the head's 128 outputs of a row, spread over
+// the G workgroups. Each publishes its partial sum through a 64-bit {tag, value} slot per
+// (head, row, workgroup) in gdn_xchg, written and polled with relaxed device-scope atomics (one
+// location carries both the tag and the value, so no fence is needed), and sums the G partials
+// in slot order, so all G workgroups apply the same factor. Tags: every call with n > t adds 1
+// to all G slots of (head, row t), so the G slots of a row always hold equal tags between calls
+// and a workgroup expects its own slot's tag + 1 from the others. The wait needs every
+// workgroup of the grid resident at once: the host launches this kernel only when 4 Hv is at
+// most the device's CU count (one workgroup per CU always fits; 8 waves, < 80 VGPRs, 16 KB LDS),
+// and falls back to the one-workgroup kernel otherwise. The polling is bounded all the same:
+// past GDN_SPIN_LIMIT polls the row's outputs are NaN instead of a hang. Block b runs head
+// b % Hv, part b / Hv: with Hv a multiple of 8 the parts of a head share an XCD.
+//
+// The slots are one table per device, so two calls must not run concurrently on one device
+// (calls on one stream, as in a decode step, are fine).
+
+__device__ unsigned long long gdn_xchg[GDN_SPLIT_MAX_HV][GDN_MAXN][GDN_SPLIT];
+
+// NT = 256: four waves, two columns per lane; NT = 512: eight waves (two per SIMD, so one wave's
+// reduction and LDS latencies hide behind the other's), one column per lane, and the v channels
+// and gates on threads of their own (256 .. 287, 288 ..) instead of a second role.
+template <int NT>
+__global__ void __launch_bounds__(NT)
+gdn_split_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
+                 const __bf16* __restrict__ b, const __bf16* __restrict__ a, long ldp,
+                 __bf16* __restrict__ ring, const __bf16* __restrict__ conv_w,
+                 const __bf16* __restrict__ A_log, const __bf16* __restrict__ dt_bias,
+                 const __bf16* __restrict__ norm_w, float* __restrict__ S,
+                 float* __restrict__ st_k, float* __restrict__ st_v, float* __restrict__ st_g,
+                 const int* __restrict__ ctl, __bf16* __restrict__ out, long ldo, int n, int Hk,
+                 int Hv, float eps) {
+  constexpr int CW = GDN_SPLIT_COLS;
+  constexpr int NC = 512 / NT;  // state columns per lane
+  __shared__ __align__(16) float sk[GDN_MAXN][GDN_D], sv[GDN_MAXN][CW];  // replayed rows
+  __shared__ __align__(16) float qa[GDN_MAXN][GDN_D], ka[GDN_MAXN][GDN_D], va[GDN_MAXN][CW];
+  __shared__ __align__(16) float oa[GDN_MAXN][CW];
+  __shared__ float sg[GDN_MAXN][2], ga[GDN_MAXN][2], l2p[GDN_MAXN][4], sst[GDN_MAXN];
+
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int j = blockIdx.x % Hv, g = blockIdx.x / Hv;
+  const int r = Hv / Hk, i = j / r;
+  const int C = 2 * Hk * GDN_D + Hv * GDN_D;
+  const int cb = g * CW;                              // first state column of this workgroup
+  const int rg = lane >> 2, lc = 4 * NC * w + NC * (lane & 3);  // rows 8 rg .., columns lc ..+NC-1
+  float* Sj = S + (size_t)j * GDN_D * GDN_D;
+
+  // Loads, all unconditional with in-bounds indices (as in the one-workgroup kernel).
+  const int P = ctl[0];
+  const int pend = min(max(ctl[1], 0), GDN_MAXN);
+  // own exchange tag of row tid & 7 (threads 0 .. n-1 use theirs)
+  const unsigned long long tagword =
+      __hip_atomic_load(&gdn_xchg[j][tid & 7][g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const bool qk_thread = tid < 2 * GDN_D;             // q (part 0) or k (part 1) channel c
+  const int part = (tid >> 7) & 1, c = tid & 127;
+  const int ch = (part * Hk + i) * GDN_D + c;
+  const int v0 = NT == 512 ? 2 * GDN_D : 0;           // v channels: threads v0 .. v0+31
+  const bool v_thread = tid >= v0 && tid < v0 + CW;
+  const int cv = tid & (CW - 1);
+  const int chv = 2 * Hk * GDN_D + j * GDN_D + cb + cv;
+  const uint2 wq = *reinterpret_cast<const uint2*>(conv_w + (size_t)ch * 4);
+  const uint2 wvv = *reinterpret_cast<const uint2*>(conv_w + (size_t)chv * 4);
+  __bf16 xb[GDN_MAXN], xbv[GDN_MAXN];
+#pragma unroll
+  for (int t = 0; t < GDN_MAXN; ++t) {
+    xb[t] = qkv[(size_t)min(t, n - 1) * ldp + ch];
+    xbv[t] = qkv[(size_t)min(t, n - 1) * ldp + chv];
+  }
+  const int gt = tid - (NT == 512 ? 2 * GDN_D + CW : 3 * 64);  // gate row of the next n threads
+  const int gtc = min(max(gt, 0), n - 1);
+  const __bf16 bb = b[(size_t)gtc * ldp + j], ab = a[(size_t)gtc * ldp + j];
+  const __bf16 dtb = dt_bias[j], alb = A_log[j];
+  const int ot = (tid >> 5) & 7, oc = tid & (CW - 1);  // output element (row ot, column cb + oc)
+  const __bf16 zb = z[(size_t)min(ot, n - 1) * ldp + j * GDN_D + cb + oc];
+  const __bf16 nwb = norm_w[cb + oc];
+  __bf16 hb[3], hbv[3];
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    const size_t slot = (size_t)((P - 3 + q) & (GDN_RING - 1)) * C;
+    hb[q] = ring[slot + ch];
+    hbv[q] = ring[slot + chv];
+  }
+  const F4 stk = *reinterpret_cast<const F4*>(st_k + ((size_t)ot * Hv + j) * GDN_D + 4 * oc);
+  const int vr = (tid >> 3) & 7, vp = tid & 7;        // staged v: row vr, columns cb + 4 vp ..
+  const F4 stv = *reinterpret_cast<const F4*>(st_v + ((size_t)vr * Hv + j) * GDN_D + cb + 4 * vp);
+  const float2 stg = *reinterpret_cast<const float2*>(st_g + ((size_t)(tid & 7) * Hv + j) * 2);
+  float s[8][NC];
+#pragma unroll
+  for (int rr = 0; rr < 8; ++rr) {
+    const float* src = Sj + (size_t)(rg * 8 + rr) * GDN_D + cb + lc;
+    if constexpr (NC == 2) {
+      const float2 v = *reinterpret_cast<const float2*>(src);
+      s[rr][0] = v.x;
+      s[rr][NC - 1] = v.y;
+    } else {
+      s[rr][0] = *src;
+    }
+  }
+
+  if (qk_thread) *reinterpret_cast<F4*>(&sk[ot][4 * oc]) = stk;
+  if (tid < 64) *reinterpret_cast<F4*>(&sv[vr][4 * vp]) = stv;
+  if (tid < GDN_MAXN) {
+    sg[tid][0] = stg.x;
+    sg[tid][1] = stg.y;
+  }
+  if (qk_thread) {
+    const bool head_writer = g == 0 && j % r == 0;  // one writer of the shared q/k ring slots
+    const float cw[4] = {lo_bf16(wq.x), hi_bf16(wq.x), lo_bf16(wq.y), hi_bf16(wq.y)};
+    float xs[3 + GDN_MAXN];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) xs[q] = P - 3 + q >= 0 ? bf16_to_f32(hb[q]) : 0.f;
+#pragma unroll
+    for (int t = 0; t < GDN_MAXN; ++t) xs[3 + t] = bf16_to_f32(xb[t]);
+#pragma unroll
+    for (int t = 0; t < GDN_MAXN; ++t) {
+      if (t < n) {
+        const float y = conv_silu(cw, xs, t);
+        (part == 0 ? qa : ka)[t][c] = y;
+        if (head_writer) ring[(size_t)((P + t) & (GDN_RING - 1)) * C + ch] = xb[t];
+        const float ss = wave_sum_fast(y * y);  // q: waves 0, 1; k: waves 2, 3
+        if (lane == 0) l2p[t][w] = ss;
+      }
+    }
+  }
+  if (v_thread) {  // the v channels of this workgroup's columns
+    const float cw[4] = {lo_bf16(wvv.x), hi_bf16(wvv.x), lo_bf16(wvv.y), hi_bf16(wvv.y)};
+    float xs[3 + GDN_MAXN];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) xs[q] = P - 3 + q >= 0 ? bf16_to_f32(hbv[q]) : 0.f;
+#pragma unroll
+    for (int t = 0; t < GDN_MAXN; ++t) xs[3 + t] = bf16_to_f32(xbv[t]);
+#pragma unroll
+    for (int t = 0; t < GDN_MAXN; ++t) {
+      if (t < n) {
+        va[t][cv] = conv_silu(cw, xs, t);
+        ring[(size_t)((P + t) & (GDN_RING - 1)) * C + chv] = xbv[t];
+      }
+    }
+  }
+  if (gt >= 0 && gt < n) {
+    const float2 gv = gate_values(bb, ab, dtb, alb);
+    ga[gt][0] = gv.x;
+    ga[gt][1] = gv.y;
+  }
+  __syncthreads();
+
+  // Stage this call's v columns for the next call (after the barrier: this workgroup's reads of
+  // the previous call's rows at the same addresses are in LDS by now; no other workgroup reads
+  // these columns). The k rows and gates, which every part of the head reads, are staged after
+  // the exchange below.
+  if (qk_thread && ot < n) st_v[((size_t)ot * Hv + j) * GDN_D + cb + oc] = va[ot][oc];
+  if (qk_thread) {
+    const float sqrt_dk = 11.313708498984761f;  // sqrt(128) rounded to fp32
+    for (int t = 0; t < n; ++t) {
+      const float ss = part == 0 ? l2p[t][0] + l2p[t][1] : l2p[t][2] + l2p[t][3];
+      const float inv = 1.0f / sqrtf(ss + 1e-6f);
+      if (part == 0) {
+        qa[t][c] = (qa[t][c] * inv) / sqrt_dk;
+      } else {
+        ka[t][c] = ka[t][c] * inv;
+      }
+    }
+  }
+
+  // ---- 1. replay, write the committed columns back ----
+  for (int t = 0; t < pend; ++t) {
+    float k[8], v[NC];
+    lds_read8(&sk[t][rg * 8], k);
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) v[cc] = sv[t][lc + cc];
+    delta_step(s, k, v, sg[t][0], sg[t][1]);
+  }
+  if (pend > 0) {
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+      float* dst = Sj + (size_t)(rg * 8 + rr) * GDN_D + cb + lc;
+      if constexpr (NC == 2) *reinterpret_cast<float2*>(dst) = make_float2(s[rr][0], s[rr][NC - 1]);
+      else *dst = s[rr][0];
+    }
+  }
+  __syncthreads();
+
+  // ---- 2. new rows on the register copy ----
+  for (int t = 0; t < n; ++t) {
+    float k[8], q[8], v[NC], o[NC];
+    lds_read8(&ka[t][rg * 8], k);
+    lds_read8(&qa[t][rg * 8], q);
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) v[cc] = va[t][lc + cc];
+    delta_step(s, k, v, ga[t][0], ga[t][1]);
+    read_out(s, q, o);
+    if (rg == 0) {
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) oa[t][lc + cc] = o[cc];
+    }
+  }
+  __syncthreads();
+
+  // ---- 3. sum of squares of the head's 128 outputs of each row, across the G workgroups ----
+  if (tid < n) {
+    const int t = tid;
+    float part_ss = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < CW; ++cc) part_ss = fmaf(oa[t][cc], oa[t][cc], part_ss);
+    const unsigned tag = (unsigned)(tagword >> 32) + 1u;
+    __hip_atomic_store(&gdn_xchg[j][t][g],
+                       ((unsigned long long)tag << 32) | __float_as_uint(part_ss),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned long long v[GDN_SPLIT];
+    bool done = false;
+    for (int it = 0; it < GDN_SPIN_LIMIT && !done; ++it) {
+#pragma unroll
+      for (int o = 0; o < GDN_SPLIT; ++o)
+        v[o] = __hip_atomic_load(&gdn_xchg[j][t][o], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      done = true;
+#pragma unroll
+      for (int o = 0; o < GDN_SPLIT; ++o) done = done && (unsigned)(v[o] >> 32) == tag;
+      if (!done) __builtin_amdgcn_s_sleep(1);
+    }
+    float tot = 0.f;
+#pragma unroll
+    for (int o = 0; o < GDN_SPLIT; ++o) tot += __uint_as_float((unsigned)v[o]);
+    sst[t] = done ? tot : __int_as_float(0x7fc00000);
+  }
+  __syncthreads();
+
+  // ---- gated RMSNorm of this workgroup's columns: thread = (row ot, column cb + oc) ----
+  if (qk_thread && ot < n) {
+    const float inv = 1.0f / sqrtf(sst[ot] / 128.0f + eps);
+    const float y = round_bf16(bf16_to_f32(nwb) * round_bf16(oa[ot][oc] * inv));
+    out[(size_t)ot * ldo + j * GDN_D + cb + oc] = f32_to_bf16(y * silu_f(bf16_to_f32(zb)));
+  }
+  // Stage the normalised k rows and the gates (part 0 of the head). Only now: every part has
+  // published its partial sum, which it does after its own loads of the previous call's staged
+  // rows at these addresses have returned.
+  if (g == 0 && qk_thread) {
+    for (int t = part; t < n; t += 2) st_k[((size_t)t * Hv + j) * GDN_D + c] = ka[t][c];
+    if (tid < n)
+      *reinterpret_cast<float2*>(st_g + ((size_t)tid * Hv + j) * 2) =
+          make_float2(ga[tid][0], ga[tid][1]);
+  }
+}
+
 }  // namespace qe
 
 using namespace qe;
+
+// Compute units of the current device, queried once per device (0 if the query fails).
+static int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = v;
+  }
+  return cus[dev];
+}
 
 extern "C" hipError_t qe_gdn_step_n(const void* qkv, const void* z, const void* b, const void* a,
                                     long ldp, void* ring, const void* conv_w, const void* A_log,
@@ -278,6 +588,19 @@ extern "C" hipError_t qe_gdn_step_n(const void* qkv, const void* z, const void* 
   if (C >= (1L << 26) || ldp < C || ldo < (long)Hv * GDN_D) return hipErrorInvalidValue;
   if (!al(S, 16) || !al(st_k, 16) || !al(st_v, 16) || !al(st_g, 8) || !al(conv_w, 8))
     return hipErrorInvalidValue;
+  // 2-8 rows: the split kernel when its whole grid fits at once; 1 row (the split gains nothing
+  // there: the exchange costs what the spread saves) and larger grids: one workgroup per head.
+  // Both give the same bits.
+  if (n >= 2 && Hv <= GDN_SPLIT_MAX_HV && Hv * GDN_SPLIT <= device_cus()) {
+    gdn_split_kernel<GDN_SPLIT_THREADS><<<dim3(Hv * GDN_SPLIT), dim3(GDN_SPLIT_THREADS), 0, stream>>>(
+        static_cast<const __bf16*>(qkv), static_cast<const __bf16*>(z),
+        static_cast<const __bf16*>(b), static_cast<const __bf16*>(a), ldp,
+        static_cast<__bf16*>(ring), static_cast<const __bf16*>(conv_w),
+        static_cast<const __bf16*>(A_log), static_cast<const __bf16*>(dt_bias),
+        static_cast<const __bf16*>(norm_w), S, st_k, st_v, st_g, ctl, static_cast<__bf16*>(out),
+        ldo, n, Hk, Hv, eps);
+    return hipGetLastError();
+  }
   gdn_step_kernel<<<dim3(Hv), dim3(GDN_THREADS), 0, stream>>>(
       static_cast<const __bf16*>(qkv), static_cast<const __bf16*>(z), static_cast<const __bf16*>(b),
       static_cast<const __bf16*>(a), ldp, static_cast<__bf16*>(ring),

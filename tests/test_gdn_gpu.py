@@ -90,7 +90,9 @@ def close(out, ref):
     return ok and frac < 0.01, d.max().item(), frac
 
 
-@pytest.mark.parametrize("hk,hv", [(16, 48), (16, 16), (2, 2), (1, 3)])
+# 2-8 rows at Hv <= 64 run the split kernel (4 workgroups per head, partial sums exchanged between
+# them); 1 row, Hv = 72 and Hv = 264 run the one-workgroup-per-head kernel.
+@pytest.mark.parametrize("hk,hv", [(16, 48), (16, 16), (2, 2), (1, 3), (9, 72), (8, 264)])
 def test_gdn_step_n_vs_oracle(native, hk, hv):
     W = weights(hk, hv, seed=hk + hv)
     g, o = gpu_layer(native, hk, hv, W), oracle_layer(hk, hv, W)
@@ -110,7 +112,7 @@ def test_gdn_step_n_vs_oracle(native, hk, hv):
     assert int(g.ctl[0]) == o.pos > 16  # the ring wrapped
 
 
-@pytest.mark.parametrize("hk,hv", [(16, 48), (2, 2)])
+@pytest.mark.parametrize("hk,hv", [(16, 48), (2, 2), (8, 264)])
 def test_gdn_lazy_rollback_bit_exact(native, hk, hv):
     W = weights(hk, hv, seed=3)
     spec, plain = gpu_layer(native, hk, hv, W), gpu_layer(native, hk, hv, W)
@@ -127,14 +129,41 @@ def test_gdn_lazy_rollback_bit_exact(native, hk, hv):
     assert torch.equal(spec.S, plain.S)
 
 
-def test_gdn_nan_isolated_to_head(native):
+@pytest.mark.parametrize("col", [5, 100])  # a column of the first / the last part of the head
+def test_gdn_nan_isolated_to_head(native, col):
     W = weights(2, 2)
     g = gpu_layer(native, 2, 2, W)
     rows = make_rows(2, 2, 1, seed=5)
-    rows[0, 2 * 256 + 128 + 5] = float("nan")  # a v channel of value head 1
+    rows[0, 2 * 256 + 128 + col] = float("nan")  # a v channel of value head 1
     out = g.run(rows, 1)
     assert torch.isnan(out[0, 128:]).all()
     assert not torch.isnan(out[0, :128]).any()
+
+
+def test_split_and_single_kernels_agree(native):
+    """A 72-head layer (always the one-workgroup kernel) and its first 64 heads as a layer of
+    their own (the split kernel for 2-8 rows, the one-workgroup kernel for 1 row), both with 8
+    value heads per qk head, give the same state and the same outputs bit for bit: the kernels
+    share the per-column arithmetic and the RMSNorm's summation order, which is what lets a call
+    pick either."""
+    hkb, hvb, hks, hvs = 9, 72, 8, 64
+    W_big = weights(hkb, hvb, seed=21)
+    D = 128
+    # the small layer's channels: q and k of the first 8 qk heads, v of the first 64 heads
+    chans = (list(range(hks * D)) + list(range(hkb * D, hkb * D + hks * D))
+             + list(range(2 * hkb * D, 2 * hkb * D + hvs * D)))
+    W_small = {"conv_w": W_big["conv_w"][chans], "A_log": W_big["A_log"][:hvs],
+               "dt_bias": W_big["dt_bias"][:hvs], "norm_w": W_big["norm_w"]}
+    big, small = gpu_layer(native, hkb, hvb, W_big), gpu_layer(native, hks, hvs, W_small)
+    idx = torch.tensor(chans, device=DEV)
+    for it, (n, kp) in enumerate([(3, 2), (8, 8), (1, 1), (5, 3), (2, 1), (1, 1)]):
+        rb = make_rows(hkb, hvb, n, seed=70 + it)
+        qkv, z, b, a = big.views(rb)
+        rs = torch.cat([qkv[:, idx], z[:, :hvs * D], b[:, :hvs], a[:, :hvs]], dim=1)
+        ob, os_ = big.run(rb, kp), small.run(rs, kp)
+        assert torch.equal(big.S[:hvs], small.S), it
+        assert torch.equal(ob[:, :hvs * D], os_), it
+    assert hvb // hkb == hvs // hks == 8
 
 
 def test_staged_rows_and_ring_match_the_oracle(native):
