@@ -19,6 +19,8 @@
 //    the MFMA layout straight into registers instead touches 16 rows x 64 bytes per instruction
 //    and measured 47% of HBM peak vs 77% this way (in_proj, 1 row, MI355X). The chunks are
 //    XOR-swizzled by row, so the ds_read_b128 of an operand is bank-conflict free.
+//  * 3-8 rows load the activation rows into registers instead (gemv_bf16_xr_kernel), so the LDS
+//    ring stays small enough for two workgroups per CU.
 //  * A workgroup holds 4 waves = 4/S row tiles x S k-parts; S grows as N shrinks so small
 //    projections still keep the CUs streaming. The S partial sums are added through LDS in the
 //    fixed order 0..S-1, so results never depend on timing.
@@ -136,6 +138,110 @@ gemv_bf16_kernel(const __bf16* __restrict__ W, const __bf16* __restrict__ x,
   }
 }
 
+// 3-8 activation rows: the same kernel with the activation rows loaded straight into registers in
+// the MFMA B-operand layout (lane 16*g4 + c: row c, k = 32*ks + 8*g4 + [0, 8) of the block), 8
+// loads of 16 bytes per lane per block, instead of staging them in LDS. The rows are tiny and
+// stay in the caches; what this saves is LDS: a workgroup keeps only its W ring (64 KB), so two
+// workgroups fit on a CU at any row count (with the rows in LDS, 3-8 rows took 88-104 KB and
+// one workgroup per CU). The MFMA operands are the same bits, so results are identical to the
+// LDS-staged kernel's. Two ring stages with their register sets are unrolled as a pair.
+template <int S>
+__global__ void __launch_bounds__(GEMV_WAVES * WAVE)
+gemv_bf16_xr_kernel(const __bf16* __restrict__ W, const __bf16* __restrict__ x,
+                    __bf16* __restrict__ out, int nr, int N, int K, long ldx, long ldo) {
+  constexpr int RT = GEMV_WAVES / S;
+  constexpr int SLOTS = GEMV_W_SLOTS;
+  constexpr int LPS = GEMV_W_SLOTS / 64 + GEMV_KB / 32;  // loads per stage: 8 W DMA + 8 x
+  extern __shared__ __attribute__((aligned(16))) u32x4_t gemv_smem[];
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int i = lane & 15, g4 = lane >> 4;
+  const int tile = blockIdx.x * RT + w / S, kp = w % S;
+  const int r0 = tile * 16;
+  const bool live = r0 < N;
+
+  const int K8 = K >> 3;
+  const int nblk = (K + GEMV_KB - 1) / GEMV_KB;
+  const int b_beg = kp * nblk / S, b_end = live ? (kp + 1) * nblk / S : b_beg;
+  const uint32_t tile_bytes = live ? (uint32_t)min(16, N - r0) * (uint32_t)K * 2u : 0u;
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc_uniform(W + (size_t)r0 * K, tile_bytes);
+  const __amdgpu_buffer_rsrc_t xrs =
+      make_rsrc_uniform(x, (uint32_t)(((size_t)(nr - 1) * ldx + K) * 2));
+  u32x4_t* ring = gemv_smem + (size_t)w * GEMV_STG * SLOTS;
+  const int cr = i < nr ? i : nr - 1;  // the activation row this lane's column reads
+  const bool xok = i < nr;
+
+  auto issue = [&](int blk, int st, u32x4_t (&xv)[GEMV_KB / 32]) __attribute__((always_inline)) {
+    u32x4_t* sb = ring + st * SLOTS;
+#pragma unroll
+    for (int j = 0; j < GEMV_W_SLOTS / 64; ++j) {
+      const int r = 2 * j + (lane >> 5), q = lane & 31;
+      buffer_load16_to_lds(wrs, (uint32_t)r * (uint32_t)K * 2u +
+                                    (uint32_t)(blk * GEMV_KB + (q ^ (r & 15)) * 8) * 2u,
+                           sb + 64 * j);
+    }
+#pragma unroll
+    for (int ks = 0; ks < GEMV_KB / 32; ++ks)
+      xv[ks] = buffer_load16(xrs, (uint32_t)(cr * ldx + blk * GEMV_KB + 32 * ks + 8 * g4) * 2u);
+  };
+  auto compute = [&](int blk, int st, const u32x4_t (&xv)[GEMV_KB / 32], f32x4_t& acc)
+      __attribute__((always_inline)) {
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    const u32x4_t* sb = ring + st * SLOTS;
+    const int cbase = blk * (GEMV_KB / 8);
+#pragma unroll
+    for (int ks = 0; ks < GEMV_KB / 32; ++ks) {
+      const int q = 4 * ks + g4;
+      const bool ok = cbase + q < K8;
+      const u32x4_t z = {0u, 0u, 0u, 0u};
+      const u32x4_t a = sb[i * 32 + (q ^ i)];
+      acc = mfma16x16x32(as_bf16x8(ok ? a : z), as_bf16x8(ok && xok ? xv[ks] : z), acc);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  u32x4_t x0[GEMV_KB / 32], x1[GEMV_KB / 32];
+  const int nb = b_end - b_beg;
+  if (nb > 0) issue(b_beg, 0, x0);
+  for (int t = 0; t < nb; t += 2) {
+    if (t + 1 < nb) {
+      issue(b_beg + t + 1, 1, x1);
+      vmcnt_wait<LPS>();
+    } else {
+      vmcnt_wait<0>();
+    }
+    compute(b_beg + t, 0, x0, acc);
+    if (t + 1 >= nb) break;
+    if (t + 2 < nb) {
+      issue(b_beg + t + 2, 0, x0);
+      vmcnt_wait<LPS>();
+    } else {
+      vmcnt_wait<0>();
+    }
+    compute(b_beg + t + 1, 1, x1, acc);
+  }
+
+  if constexpr (S > 1) {
+    __shared__ f32x4_t red[GEMV_WAVES][WAVE];
+    red[w][lane] = acc;
+    __syncthreads();
+    if (kp != 0) return;
+#pragma unroll
+    for (int v = 1; v < S; ++v) acc += red[w + v][lane];  // ((p0 + p1) + p2) + ...
+  }
+  if (i < nr) {
+    __bf16* op = out + (size_t)i * ldo;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = r0 + 4 * g4 + j;
+      if (row < N) op[row] = f32_to_bf16(acc[j]);
+    }
+  }
+}
+
 // Achievable streaming-read bandwidth: each workgroup reads one contiguous range of the buffer,
 // its 256 threads 16 bytes each per step (4 KB contiguous per workgroup step), 8 steps in flight,
 // non-temporal. The loads are folded into a value that is stored only if it equals a constant,
@@ -174,6 +280,21 @@ static hipError_t launch_gemv(const __bf16* W, const __bf16* x, __bf16* out, int
   if (attr != hipSuccess) return attr;
   const int tiles = (N + 15) / 16;
   gemv_bf16_kernel<S, XI><<<dim3((tiles + RT - 1) / RT), dim3(GEMV_WAVES * WAVE), lds, stream>>>(
+      W, x, out, nr, N, K, ldx, ldo);
+  return hipGetLastError();
+}
+
+template <int S>
+static hipError_t launch_gemv_xr(const __bf16* W, const __bf16* x, __bf16* out, int nr, int N,
+                                 int K, long ldx, long ldo, hipStream_t stream) {
+  constexpr int RT = GEMV_WAVES / S;
+  constexpr size_t lds = (size_t)GEMV_WAVES * GEMV_STG * GEMV_W_SLOTS * 16;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_bf16_xr_kernel<S>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (attr != hipSuccess) return attr;
+  const int tiles = (N + 15) / 16;
+  gemv_bf16_xr_kernel<S><<<dim3((tiles + RT - 1) / RT), dim3(GEMV_WAVES * WAVE), lds, stream>>>(
       W, x, out, nr, N, K, ldx, ldo);
   return hipGetLastError();
 }
@@ -219,6 +340,13 @@ extern "C" hipError_t qe_gemv_bf16(const void* W, const void* x, void* out, int 
   const auto* xb = static_cast<const __bf16*>(x);
   auto* ob = static_cast<__bf16*>(out);
   const int S = qe_gemv_kparts(N, K);
+  if (nr >= 3) {  // activation rows in registers: two workgroups per CU at any row count
+    switch (S) {
+      case 1: return launch_gemv_xr<1>(Wb, xb, ob, nr, N, K, ldx, ldo, stream);
+      case 2: return launch_gemv_xr<2>(Wb, xb, ob, nr, N, K, ldx, ldo, stream);
+      default: return launch_gemv_xr<4>(Wb, xb, ob, nr, N, K, ldx, ldo, stream);
+    }
+  }
   switch ((nr + 1) / 2) {
     case 1: return launch_gemv_s<1>(S, Wb, xb, ob, nr, N, K, ldx, ldo, stream);
     case 2: return launch_gemv_s<2>(S, Wb, xb, ob, nr, N, K, ldx, ldo, stream);
