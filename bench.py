@@ -275,6 +275,35 @@ def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
                                        "GBps": round(alg_bytes_layer(L, n) / (us * 1e3), 1)}
     del kcs, vcs
 
+    # MTP verify at 8 rows (7 drafts) at pos 4096 and 16384, on bf16 and on fp8 caches: 48 columns
+    # at GQA 6, the multi-column kernel (its fp8 mode for the second)
+    def codes(L):
+        c = torch.randint(0, 256, (HKV, L, D), device=dev, generator=gen, dtype=torch.int32)
+        c = torch.where((c & 0x7F) == 0x7F, c ^ 1, c)  # no NaN codes
+        return c.to(torch.uint8).view(torch.float8_e4m3fn)
+    for P in (4096, 16384):
+        L, n, nl = P + 8, 8, 16
+        q8, qg8 = rnd(n, HQ * D), rnd(n, HQ * 2 * D)
+        out8 = torch.empty(n, HQ * D, dtype=BF, device=dev)
+        ns = qa.default_splits(L, HKV)
+        po8, pml8 = qa.alloc_partials(n, HQ, ns, dev)
+        pos8 = torch.tensor([P], dtype=torch.int32, device=dev)
+        for fp8 in (False, True):
+            kcs = [codes(L) if fp8 else rnd(HKV, L, D) for _ in range(nl)]
+            vcs = [codes(L) if fp8 else rnd(HKV, L, D) for _ in range(nl)]
+
+            def verify8():
+                for kk, vv in zip(kcs, vcs):
+                    if fp8:
+                        C.attn_decode_fp8(q8, kk, vv, pos8, qg8, po8, pml8, out8, 1 / 16, 1 / 16)
+                    else:
+                        C.attn_decode(q8, kk, vv, pos8, qg8, po8, pml8, out8)
+            us = time_fn_graph(torch, verify8, steps, warmup) * 1e3 / nl
+            nbytes = (2048 * L + 36864 * n) if fp8 else alg_bytes_layer(L, n)
+            res[f"{'fp8kv_' if fp8 else ''}verify_8rows_{P // 1024}k"] = {
+                "us_per_layer": round(us, 3), "GBps": round(nbytes / (us * 1e3), 1)}
+            del kcs, vcs
+
     # cfg 4: KV 131072 (537 MB per layer: two layers rotate past the Infinity Cache), plus the
     # variant with 1% of key rows scaled by 8
     L, nl = 131072, 2

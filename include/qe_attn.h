@@ -116,7 +116,7 @@ hipError_t qe_attn_prep_fp8(const void* qg, const void* k, const void* v, long l
 
 /* qe_attn_decode over the fp8 cache: the same attention on the dequantized values (k_scale
  * scales every score, v_scale the attention output before its bf16 rounding). Row t of an n-row
- * call is bit-identical to a 1-row call. Valid as qe_attn_decode with (Hq/Hkv)*n <= 32. */
+ * call is bit-identical to a 1-row call. Valid as qe_attn_decode. */
 hipError_t qe_attn_decode_fp8(const void* q, const void* kc8, const void* vc8, const int* pos,
                               const void* qg, long ldp, float* part_o, float* part_ml, void* out,
                               long ldo, int n, int Hq, int Hkv, int max_len, int NS, float scale,

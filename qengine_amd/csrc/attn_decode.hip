@@ -645,7 +645,10 @@ constexpr int TILE_U4 = TILE * ROW_CHUNKS;   // 16-byte slots of one K (or V) ti
 constexpr int REGION_U4 = 2 * TILE_U4;       // a subset's K tile then V tile
 }  // namespace cols
 
-template <int NT, int CPW>
+// KV8: an fp8 cache (E4M3FN codes). The subset's K tile goes to LDS in the swizzled 256-byte-row
+// layout of load_tile8 (read by qk_tile8), its V tile row-major; both are 8 KB and convert to the
+// same bf16 operands exactly, so the tile arithmetic below is unchanged.
+template <int NT, int CPW, bool KV8 = false>
 __global__ void __launch_bounds__(cols::SUBSETS * (NT / CPW) * WAVE)
 attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
                           const __bf16* __restrict__ vc, const int* __restrict__ pos_ptr,
@@ -688,9 +691,10 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
 
   __shared__ __attribute__((aligned(16))) u32x4_t lds[SUB * cols::REGION_U4];  // 128 KB
   __shared__ float s_m[SUB][16 * NT], s_l[SUB][16 * NT];
-  const size_t head_off = (size_t)g * max_len * HD;
+  constexpr int ELEM = KV8 ? 1 : 2;  // bytes per cache value
+  const size_t head_off = (size_t)g * max_len * HD * ELEM;  // bytes
   u32x4_t* kt = lds + sub * cols::REGION_U4;
-  const u32x4_t* vt = kt + cols::TILE_U4;
+  const u32x4_t* vt = kt + (KV8 ? cols::TILE_U4 / 2 : cols::TILE_U4);
 
   // One pass, inlined once per call of the lambda (a loop over passes would keep the merge's
   // loop-invariant addresses live through the tile rounds and spill).
@@ -700,9 +704,11 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
     for (int u = 0; u < CPW; ++u)
       Lcol[u] = in_pass((rank * CPW + u) * 16 + c, grp, P)
                     ? min(pos0 + ((rank * CPW + u) * 16 + c) / grp + 1, max_len) : 0;
-    const uint32_t bytes = (uint32_t)P.end * (uint32_t)(HD * 2);
-    const __amdgpu_buffer_rsrc_t krs = make_rsrc_uniform(kc + head_off, bytes);
-    const __amdgpu_buffer_rsrc_t vrs = make_rsrc_uniform(vc + head_off, bytes);
+    const uint32_t bytes = (uint32_t)P.end * (uint32_t)(HD * ELEM);
+    const __amdgpu_buffer_rsrc_t krs =
+        make_rsrc_uniform(reinterpret_cast<const char*>(kc) + head_off, bytes);
+    const __amdgpu_buffer_rsrc_t vrs =
+        make_rsrc_uniform(reinterpret_cast<const char*>(vc) + head_off, bytes);
 
     float m[CPW], l[CPW];
     f32x4_t acc[CPW][16];
@@ -719,7 +725,19 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
     for (int r = 0; r < rounds; ++r) {
       const int p0 = P.beg + (r * SUB + sub) * TILE;  // this subset's tile in round r
       const bool has = p0 < P.end;                     // uniform per subset
-      if (has) {
+      if (has && KV8) {
+        // fp8: 8 loads of K (rows 4j .. 4j+3, chunks swizzled as in load_tile8) and 8 of V
+        // (row-major), one KB each, shared by the subset's waves.
+        for (int i = rank; i < 16; i += WPS) {
+          const int j = i & 7, row = 4 * j + (lane >> 4);
+          if (i < 8)
+            buffer_load16_to_lds(krs, (uint32_t)(p0 + row) * HD + ((lane & 15) ^ (row & 15)) * 16,
+                                 kt + 64 * j);
+          else
+            buffer_load16_to_lds(vrs, (uint32_t)(p0 + row) * HD + (lane & 15) * 16,
+                                 kt + cols::TILE_U4 / 2 + 64 * j);
+        }
+      } else if (has) {
         // The subset's WPS waves share its 32 LDS-DMA loads: 16 of K (rows 2i, 2i+1, swizzled as
         // k_slot) and 16 of V (row-major), one KB of contiguous cache each.
         for (int i = rank; i < 32; i += WPS) {
@@ -736,7 +754,8 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
       __syncthreads();  // every wave's loads of this round have landed
       if (has) {
         f32x4_t sacc[CPW][2];
-        tile::qk_tile<CPW>(kt, qb, c, g4, sacc);
+        if constexpr (KV8) qk_tile8<CPW>(kt, qb, c, g4, sacc);
+        else tile::qk_tile<CPW>(kt, qb, c, g4, sacc);
         u32x4_t pb_hi[CPW], pb_lo[CPW];
         if (p0 + TILE > P.Lmin)
           tile::softmax_tile<CPW, true, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
@@ -746,8 +765,14 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
         for (int hh = 0; hh < 2; ++hh) {
           u32x4_t vr[8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            vr[e] = vt[(16 * (e >> 2) + 4 * g4 + (e & 3)) * ROW_CHUNKS + 16 * hh + c];
+          for (int e = 0; e < 8; ++e) {
+            const int row = 16 * (e >> 2) + 4 * g4 + (e & 3);
+            if constexpr (KV8)
+              vr[e] = fp8x8_to_bf16x8(*reinterpret_cast<const u32x2_t*>(
+                  reinterpret_cast<const char*>(vt) + row * HD + 128 * hh + 8 * c));
+            else
+              vr[e] = vt[row * ROW_CHUNKS + 16 * hh + c];
+          }
           tile::pv_half<CPW, true>(vr, hh, pb_hi, pb_lo, acc);
         }
       }
@@ -935,13 +960,16 @@ static hipError_t launch_partials(const void* q, const void* kc, const void* vc,
   const auto* K = static_cast<const __bf16*>(kc);
   const auto* V = static_cast<const __bf16*>(vc);
   if (kv8) {
-    if (NT > 2) return hipErrorInvalidValue;  // the multi-row cols kernel reads bf16 only
     if (NT == 1 && n == 1)
       attn_partials_kernel<1, false, false, true><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{});
     else if (NT == 1)
       attn_partials_kernel<1, false, true, true><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{});
-    else
+    else if (NT == 2)
       attn_partials_kernel<2, false, true, true><<<grid, dim3(waves_for<2>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{});
+    else if (NT == 3)
+      attn_partials_cols_kernel<3, 1, true><<<grid, dim3(cols::SUBSETS * 3 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2);
+    else
+      attn_partials_cols_kernel<4, 2, true><<<grid, dim3(cols::SUBSETS * 2 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2);
     return hipGetLastError();
   }
   // NT = 1, 2: every wave holds all column tiles (measured fastest at 1-5 rows, GQA 6).
@@ -1021,7 +1049,7 @@ extern "C" hipError_t qe_attn_decode_fp8_partials(const void* q, const void* kc8
                                                   hipStream_t stream) {
   hipError_t e = check_decode_shape(n, Hq, Hkv, max_len, NS);
   if (e != hipSuccess) return e;
-  if ((Hq / Hkv) * n > 32 || !kv_scales_ok(k_scale, 1.f)) return hipErrorInvalidValue;
+  if (!kv_scales_ok(k_scale, 1.f)) return hipErrorInvalidValue;
   if (!aligned16(q) || !aligned16(kc8) || !aligned16(vc8) || !aligned16(part_o) || !pos ||
       !part_ml)
     return hipErrorInvalidValue;

@@ -148,8 +148,7 @@ DecodeArgs parse_decode(const torch::Tensor& q, const torch::Tensor& kc, const t
                   QG.w == (long)Hq * 2 * HD,
               "part_ml must be [>=n, Hq, NS, 2]; out width Hq*256; qg width Hq*512");
   TORCH_CHECK(n >= 1 && n <= 8, "decode takes 1..8 rows");
-  TORCH_CHECK((Hq / Hkv) * n <= (kv8 ? 32 : 64),
-              "GQA group size * rows must be <= ", kv8 ? 32 : 64, kv8 ? " with the fp8 cache" : "");
+  TORCH_CHECK((Hq / Hkv) * n <= 64, "GQA group size * rows must be <= 64");
   TORCH_CHECK(NS >= 1, "part_o needs at least one split");
   return {n, Hq, Hkv, max_len, NS, QG.ld, O.ld};
 }

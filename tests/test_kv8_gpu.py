@@ -6,7 +6,8 @@
     conversion;
   * with any scales it is within the decode tolerance of the oracle's attention over the
     dequantized cache (per element |out-ref| <= 2^-6|ref| + 2e-3, max-abs 2e-2, mean-abs 2e-3);
-  * rows of a multi-row call are bit-identical to 1-row calls."""
+  * rows of a multi-row call are bit-identical to 1-row calls, including the 6-8-row verify
+    shapes that run the multi-column kernel's fp8 mode."""
 import numpy as np
 import pytest
 import torch
@@ -121,8 +122,32 @@ def test_prep_fp8_writes_the_oracle_codes(native, ks, vs):
         assert int(cache8.view(torch.uint8)[:, : pos].count_nonzero()) == 0  # nothing else written
 
 
-def test_fp8_rejects_wide_verify_shapes(native):
-    case = decode_case(seed=1, hq=24, hkv=4, pos=100, n=6, max_len=200)
+# 6-8 rows at GQA 6 and 8 (36-64 columns) run the multi-column kernel's fp8 mode
+@pytest.mark.parametrize("hq,hkv,n,pos,max_len,ns", [
+    (24, 4, 6, 4090, 4096, 64), (24, 4, 8, 1000, 1100, 64), (24, 4, 7, 16370, 16384, 64),
+    (32, 4, 8, 600, 640, 16), (24, 4, 6, 2045, 2100, 64)])
+def test_fp8_wide_verify_scale_one_equals_bf16(native, hq, hkv, n, pos, max_len, ns):
+    case = decode_case(seed=pos + 7 * n, hq=hq, hkv=hkv, pos=pos, n=n, max_len=max_len)
     kc8, vc8 = quantize_cache(case.kc, 1.0), quantize_cache(case.vc, 1.0)
-    with pytest.raises(RuntimeError, match="32"):
-        run_fp8(native, case.q, case.qg, kc8, vc8, case.pos, 8, 1.0, 1.0)
+    kd = K8.dequantize(kc8.view(torch.uint8), 1.0).to(BF)
+    vd = K8.dequantize(vc8.view(torch.uint8), 1.0).to(BF)
+    a = run_fp8(native, case.q, case.qg, kc8, vc8, case.pos, ns, 1.0, 1.0)
+    b = run_bf16(native, case.q, case.qg, kd, vd, case.pos, ns)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("ks,vs", [(0.5, 0.25), (0.037, 0.011)])
+def test_fp8_wide_verify_vs_oracle_and_rows(native, ks, vs):
+    """8 rows at GQA 6 against the oracle on the dequantized cache, and every row bit-identical
+    to a 1-row call (which runs the one-tile kernel)."""
+    n, pos, max_len = 8, 3000, 3010
+    case = decode_case(seed=int(ks * 1e4), hq=24, hkv=4, pos=pos, n=n, max_len=max_len)
+    kc8, vc8 = quantize_cache(case.kc, ks), quantize_cache(case.vc, vs)
+    out = run_fp8(native, case.q, case.qg, kc8, vc8, case.pos, 64, ks, vs)
+    ref = O.attn_decode(case.q, K8.dequantize(kc8.view(torch.uint8), ks),
+                        K8.dequantize(vc8.view(torch.uint8), vs), case.pos, case.qg, case.hq)
+    ok, mx, mean = attn_close(out, ref)
+    assert ok, (mx, mean)
+    for t in range(n):
+        o1 = run_fp8(native, case.q[t:t + 1], case.qg[t:t + 1], kc8, vc8, case.pos + t, 64, ks, vs)
+        assert torch.equal(o1[0], out[t]), t
