@@ -9,7 +9,10 @@ Parity status per function (each is pinned by checks in ``tests/test_oracle.py``
   rope_inv_freq, rope_cos_sin, apply_rope, rmsnorm1p, attention_qkv_from_proj,
   attention_core, attention_core_grouped, attn_prep, attn_decode, attn_prefill,
   flash_decode_fp64                                   -> pinned (closed forms, brute force,
-                                                         invariants, bf16 rounding model)
+                                                         invariants, bf16 rounding model; the
+                                                         whole layer against HF transformers'
+                                                         Qwen3_5Attention in
+                                                         tests/test_oracle_hf.py)
   gemv_exact, gemv_bound, gemv_bf16_ref               -> pinned (brute-force loops, one-hot and
                                                          identity closed forms, NaN, the bound)
   step_oracle: embed, residual_rmsnorm1p, swiglu, argmax, accept, commit, mtp_select
