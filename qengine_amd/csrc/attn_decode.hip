@@ -739,14 +739,14 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
         }
       } else if (has) {
         // The subset's WPS waves share its 32 LDS-DMA loads: 16 of K (rows 2i, 2i+1, swizzled as
-        // k_slot) and 16 of V (row-major), one KB of contiguous cache each.
+        // k_slot) and 16 of V (swizzled as tile::v_swz), one KB of contiguous cache each.
         for (int i = rank; i < 32; i += WPS) {
           const int j = i & 15, row = 2 * j + (lane >> 5);
           if (i < 16)
             buffer_load16_to_lds(krs, (uint32_t)(p0 + row) * (HD * 2) + ((lane & 31) ^ (row & 15)) * 16,
                                  kt + 2 * j * ROW_CHUNKS);
           else
-            buffer_load16_to_lds(vrs, (uint32_t)(p0 + row) * (HD * 2) + (lane & 31) * 16,
+            buffer_load16_to_lds(vrs, (uint32_t)(p0 + row) * (HD * 2) + ((lane & 31) ^ tile::v_swz(row)) * 16,
                                  kt + cols::TILE_U4 + 2 * j * ROW_CHUNKS);
         }
       }
@@ -761,19 +761,20 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
           tile::softmax_tile<CPW, true, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
         else
           tile::softmax_tile<CPW, false, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
+        if constexpr (KV8) {
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          u32x4_t vr[8];
+          for (int hh = 0; hh < 2; ++hh) {
+            u32x4_t vr[8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int row = 16 * (e >> 2) + 4 * g4 + (e & 3);
-            if constexpr (KV8)
+            for (int e = 0; e < 8; ++e) {
+              const int row = 16 * (e >> 2) + 4 * g4 + (e & 3);
               vr[e] = fp8x8_to_bf16x8(*reinterpret_cast<const u32x2_t*>(
                   reinterpret_cast<const char*>(vt) + row * HD + 128 * hh + 8 * c));
-            else
-              vr[e] = vt[row * ROW_CHUNKS + 16 * hh + c];
+            }
+            tile::pv_half<CPW, true>(vr, hh, pb_hi, pb_lo, acc);
           }
-          tile::pv_half<CPW, true>(vr, hh, pb_hi, pb_lo, acc);
+        } else {
+          tile::pv_tile_tr<CPW, true>(vt, lane, g4, pb_hi, pb_lo, acc);
         }
       }
       __syncthreads();  // this round's tiles are read before the next round overwrites them
@@ -823,21 +824,30 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
         }
         __syncthreads();
         if (mine) {
-          const int h = sub >> 1, i0 = 4 * (sub & 1);
+          // thread (sub, lane) merges accumulators 4 sub .. 4 sub + 3 over the subsets in order
           f32x4_t mo[4];
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             f32x4_t sum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int v = 0; v < SUB; ++v) sum += s_acc[v][8 * h + i0 + k][lane] * wsc[u][v];
+            for (int v = 0; v < SUB; ++v) sum += s_acc[v][4 * sub + k][lane] * wsc[u][v];
             mo[k] = sum;
           }
           const int t = col / grp, head = g * grp + (col - t * grp);
-          float* dst = part_o + (((size_t)t * Hq + head) * NS + s) * HD + 128 * h + 32 * g4 + i0;
+          float* dst = part_o + (((size_t)t * Hq + head) * NS + s) * HD;
+          if constexpr (KV8) {
+            // acc[8hh + i][ii] = O^T[128hh + 32g4 + 8ii + i] (tile::pv_half)
+            const int h = sub >> 1, i0 = 4 * (sub & 1);
 #pragma unroll
-          for (int ii = 0; ii < 4; ++ii)
-            reinterpret_cast<f32x4_t*>(dst + 8 * ii)[0] =
-                f32x4_t{mo[0][ii], mo[1][ii], mo[2][ii], mo[3][ii]};
+            for (int ii = 0; ii < 4; ++ii)
+              reinterpret_cast<f32x4_t*>(dst + 128 * h + 32 * g4 + i0 + 8 * ii)[0] =
+                  f32x4_t{mo[0][ii], mo[1][ii], mo[2][ii], mo[3][ii]};
+          } else {
+            // acc[i][k] = O^T[16i + 4g4 + k] (tile::pv_tile_tr)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+              reinterpret_cast<f32x4_t*>(dst + 16 * (4 * sub + k) + 4 * g4)[0] = mo[k];
+          }
         }
         __syncthreads();  // (also ends the pass: the next pass's loads may overwrite `lds`)
       }

@@ -52,11 +52,6 @@ static_assert(LOAD_ROWS % 2 == 0 && LOADS_PER_TILE * AHEAD < 64, "tile split ove
 constexpr int PF_CPOL = 0;                      // cached loads: every row block re-reads its KV head
 constexpr int XCDS = 8;                         // MI355X: 8 XCDs, each with its own L2
 
-// V tile: chunk q of row r sits in slot r * ROW_CHUNKS + (q ^ v_swz(r)). A transposing read of
-// the PV operand touches 16 rows at the same two chunks; with this swizzle every 8 consecutive
-// rows spread them over 16 distinct 16-byte bank groups.
-__device__ __forceinline__ int v_swz(int r) { return 2 * (r & 7); }
-
 // Issue this wave's LDS-DMA loads of tile [p0, p0 + 32): rows LOAD_ROWS*w .. +LOAD_ROWS of K
 // and of V (both swizzled: lane i fetches the chunk that belongs in slot 64j + i).
 __device__ __forceinline__ void issue_tile(u32x4_t* stage, __amdgpu_buffer_rsrc_t krs,
@@ -71,7 +66,7 @@ __device__ __forceinline__ void issue_tile(u32x4_t* stage, __amdgpu_buffer_rsrc_
 #pragma unroll
   for (int j = 0; j < LOAD_INSTR; ++j) {
     const int r = LOAD_ROWS * w + 2 * j + (lane >> 5);
-    buffer_load16_to_lds<PF_CPOL>(vrs, (uint32_t)(p0 + r) * (HD * 2) + ((lane & 31) ^ v_swz(r)) * 16,
+    buffer_load16_to_lds<PF_CPOL>(vrs, (uint32_t)(p0 + r) * (HD * 2) + ((lane & 31) ^ tile::v_swz(r)) * 16,
                                   stage + TILE_U4 + (LOAD_ROWS * w + 2 * j) * ROW_CHUNKS);
   }
 }
@@ -79,40 +74,8 @@ __device__ __forceinline__ void issue_tile(u32x4_t* stage, __amdgpu_buffer_rsrc_
 // Per-wave running softmax state and O^T accumulators.
 struct WaveState {
   float m[NT], l[NT];
-  f32x4_t acc[NT][16];  // acc[ct][i][k] = O^T[16i + 4 g4 + k][column ct*16 + c]
+  f32x4_t acc[NT][16];  // acc[ct][i][k] = O^T[16i + 4 g4 + k][column ct*16 + c] (tile::pv_tile_tr)
 };
-
-// O^T += V^T P^T over one tile. M-tile i holds dims 16i .. 16i+15, and the A operand of lane
-// (c, g4) is V[P(g4, e)][16i + c] for e = 0..7, P(g4, e) = p0 + 16(e>>2) + 4g4 + (e&3) (the
-// positions of P^T's element e, tile::softmax_tile). ds_read_b64_tr_b16 hands lane 4a + b of each
-// 16-lane group element b of the 8 bytes addressed by lane a + 4e of the group, as element e
-// (lane layout checked on MI355X). So lane (a, ep = lane/4 & 3, g4) addresses V row 4g4 + ep
-// (+16 for elements 4..7) at dims 16i + 4a .. +3.
-template <bool SPLIT>
-__device__ __forceinline__ void pv_tile(const u32x4_t* vt, int lane, int g4,
-                                        const u32x4_t (&pb_hi)[NT], const u32x4_t (&pb_lo)[NT],
-                                        f32x4_t (&acc)[NT][16]) {
-  typedef short v4i16 __attribute__((ext_vector_type(4)));
-  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-  const int a = lane & 3, r = 4 * g4 + ((lane >> 2) & 3);
-  char* vb = const_cast<char*>(reinterpret_cast<const char*>(vt)) + r * (HD * 2) + (a & 1) * 8;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    char* p = vb + ((2 * i + (a >> 1)) ^ v_swz(r)) * 16;  // rows r and r + 16 share the swizzle
-    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        reinterpret_cast<lds_v4i16*>((__attribute__((address_space(3))) char*)p));
-    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        reinterpret_cast<lds_v4i16*>((__attribute__((address_space(3))) char*)(p + 16 * HD * 2)));
-    const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
-    const u32x4_t av = {l2[0], l2[1], h2[0], h2[1]};
-#pragma unroll
-    for (int ct = 0; ct < NT; ++ct) {
-      acc[ct][i] = mfma16x16x32(as_bf16x8(av), as_bf16x8(pb_hi[ct]), acc[ct][i]);
-      if constexpr (SPLIT)
-        acc[ct][i] = mfma16x16x32(as_bf16x8(av), as_bf16x8(pb_lo[ct]), acc[ct][i]);
-    }
-  }
-}
 
 // Tiles [j0, j1) of the ring with one branch-free body (SPLIT and MASK fixed).
 template <bool SPLIT, bool MASK>
@@ -134,7 +97,7 @@ __device__ __forceinline__ void run_tiles(int j0, int j1, int Lwave, u32x4_t* ld
     u32x4_t pb_hi[NT], pb_lo[NT];
     tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc, pb_hi,
                                         pb_lo);
-    pv_tile<SPLIT>(vt, lane, g4, pb_hi, pb_lo, st.acc);
+    tile::pv_tile_tr<NT, SPLIT>(vt, lane, g4, pb_hi, pb_lo, st.acc);
   }
 }
 

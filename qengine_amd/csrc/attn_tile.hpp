@@ -124,5 +124,43 @@ __device__ __forceinline__ void pv_half(const u32x4_t (&vr)[8], int hh, const u3
   }
 }
 
+// A V tile (32 rows of 256 bf16) in LDS for pv_tile_tr: chunk q of row r sits in 16-byte slot
+// r * ROW_CHUNKS + (q ^ v_swz(r)). A transposing read touches 16 rows at the same two chunks; with
+// this swizzle every 8 consecutive rows spread them over 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int v_swz(int r) { return 2 * (r & 7); }
+
+// O^T += V^T P^T over one tile with the V^T operands read from LDS by gfx950's transposing read.
+// M-tile i holds dims 16i .. 16i+15: acc[ct][i][k] = O^T[16i + 4 g4 + k][column c]. The A operand
+// of lane (c, g4) is V[P(g4, e)][16i + c] for e = 0..7, P(g4, e) = p0 + 16(e>>2) + 4g4 + (e&3)
+// (the positions of P^T's element e, softmax_tile). ds_read_b64_tr_b16 hands lane 4a + b of each
+// 16-lane group element b of the 8 bytes addressed by lane a + 4e of the group, as element e
+// (lane layout checked on MI355X). So lane (a = lane & 3, lane/4 & 3, g4) addresses V row
+// 4g4 + (lane/4 & 3) (+16 for elements 4..7) at dims 16i + 4a .. +3.
+template <int NT, bool SPLIT>
+__device__ __forceinline__ void pv_tile_tr(const u32x4_t* vt, int lane, int g4,
+                                           const u32x4_t (&pb_hi)[NT], const u32x4_t (&pb_lo)[NT],
+                                           f32x4_t (&acc)[NT][16]) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  const int a = lane & 3, r = 4 * g4 + ((lane >> 2) & 3);
+  char* vb = const_cast<char*>(reinterpret_cast<const char*>(vt)) + r * (HD * 2) + (a & 1) * 8;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    char* p = vb + ((2 * i + (a >> 1)) ^ v_swz(r)) * 16;  // rows r and r + 16 share the swizzle
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        reinterpret_cast<lds_v4i16*>((__attribute__((address_space(3))) char*)p));
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        reinterpret_cast<lds_v4i16*>((__attribute__((address_space(3))) char*)(p + 16 * HD * 2)));
+    const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
+    const u32x4_t av = {l2[0], l2[1], h2[0], h2[1]};
+#pragma unroll
+    for (int ct = 0; ct < NT; ++ct) {
+      acc[ct][i] = mfma16x16x32(as_bf16x8(av), as_bf16x8(pb_hi[ct]), acc[ct][i]);
+      if constexpr (SPLIT)
+        acc[ct][i] = mfma16x16x32(as_bf16x8(av), as_bf16x8(pb_lo[ct]), acc[ct][i]);
+    }
+  }
+}
+
 }  // namespace tile
 }  // namespace qe
