@@ -711,7 +711,7 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
         make_rsrc_uniform(reinterpret_cast<const char*>(vc) + head_off, bytes);
 
     float m[CPW], l[CPW];
-    f32x4_t acc[CPW][16];
+    f32x4_t acc[CPW][16];  // bf16: tile::pv_tile_tr layout; fp8: tile::pv_half layout
 #pragma unroll
     for (int u = 0; u < CPW; ++u) {
       m[u] = -INFINITY;

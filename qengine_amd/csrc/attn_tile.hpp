@@ -104,7 +104,8 @@ __device__ __forceinline__ void softmax_tile(const f32x4_t (&sacc)[NT][2], int p
   }
 }
 
-// O^T += V^T P^T for dims [128hh, 128hh + 128) (the prefill layout): vr[e] = 16 bytes of V row
+// O^T += V^T P^T for dims [128hh, 128hh + 128) from V rows in registers (the decode kernels' V
+// loads, and the fp8 cache's converted codes): vr[e] = 16 bytes of V row
 // P(g4, e), dims 128hh + 8c + [0, 8). M-tile i of the half has row c = dim 128hh + 8c + i, so
 // acc[ct][8hh + i][ii] = O^T[dim 128hh + 32g4 + 8ii + i][column c].
 template <int NT, bool SPLIT>
