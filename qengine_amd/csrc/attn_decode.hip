@@ -982,8 +982,16 @@ static hipError_t launch_partials(const void* q, const void* kc, const void* vc,
       attn_partials_cols_kernel<4, 2, true><<<grid, dim3(cols::SUBSETS * 2 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2);
     return hipGetLastError();
   }
-  // NT = 1, 2: every wave holds all column tiles (measured fastest at 1-5 rows, GQA 6).
+  // NT = 1, 2: every wave holds all column tiles (measured fastest at 1-5 rows, GQA 6), except
+  // NT = 2 on caches whose slices hold at most 4 tiles (max_len <= 128 NS): there the 4 waves of
+  // attn_partials_kernel<2> leave half the CU idle, and the multi-column kernel (one column tile
+  // per wave, 8 waves) measured 7-10% faster at 4k-8k (it is 3-10% slower on 8-16-tile slices).
+  // The two give the same bits per column.
   // NT = 3, 4: one subset wave per column tile (the one-tile kernel would spill: 2.3-2.8x slower).
+  if (NT == 2 && split_size(max_len, nd) <= 4 * TILE) {
+    attn_partials_cols_kernel<2, 1><<<grid, dim3(cols::SUBSETS * 2 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2);
+    return hipGetLastError();
+  }
   switch (NT) {
     case 1:
       if (n == 1)
