@@ -8,6 +8,8 @@ Bars:
   rows   : row t of an n-row call is bit-identical to a 1-row call at position pos+t
            (reference tests/test_kernels.py:354-357); MTP verify argmax == sequential decodes.
 """
+import copy
+
 import pytest
 import torch
 
@@ -221,6 +223,25 @@ def test_rows_straddling_a_slice_size_change(native, hq, hkv, n, pos, ns):
     for t in range(n):
         o1 = gpu_decode(native, case, ns, pos=case.pos + t, rows=slice(t, t + 1))
         assert torch.equal(o1[0], out[t]), t
+
+
+@pytest.mark.parametrize("n", [3, 5])
+def test_two_tile_kernels_give_the_same_bits(native, n):
+    """3-5 rows (two MFMA column tiles) take the multi-column kernel when every slice of the cache
+    holds at most 4 tiles (max_len <= 128 NS) and the two-tile kernel otherwise. The same call on
+    caches of 8192 and 8193 positions (NS = 64) attends the same positions through both kernels:
+    the outputs are equal bit for bit, match the oracle, and each row equals a 1-row call."""
+    case = decode_case(seed=40 + n, hq=24, hkv=4, pos=8000, n=n, max_len=8193)
+    short = copy.copy(case)
+    short.kc, short.vc = case.kc[:, :8192].contiguous(), case.vc[:, :8192].contiguous()
+    out_long = gpu_decode(native, case, 64)
+    out_short = gpu_decode(native, short, 64)
+    assert torch.equal(out_long, out_short)
+    ok, mx, mean = attn_close(out_short, oracle_decode(short))
+    assert ok, (mx, mean)
+    for t in range(n):
+        o1 = gpu_decode(native, short, 64, pos=case.pos + t, rows=slice(t, t + 1))
+        assert torch.equal(o1[0], out_short[t]), t
 
 
 @pytest.mark.parametrize("n,pos", [(1, 1000), (5, 3000), (8, 200)])
