@@ -97,3 +97,36 @@ def test_config5_chunked_prefill(native):
     torch.cuda.synchronize()
     ok, mx, mean = attn_close(out.cpu(), ref)
     assert ok, (mx, mean)
+
+
+@pytest.mark.parametrize("T", [9, 40, 1001])
+def test_prep_chunk_equals_eight_row_preps(native, T):
+    """attn_prep_chunk takes 8 rows per workgroup with a shared rotary table; attn_prep over the
+    same rows in calls of at most 8 rows takes one row per workgroup. q_out and the written cache
+    rows are equal bit for bit, including a ragged last block."""
+    C = native
+    hq, hkv, pos = 24, 4, 300
+    max_len = pos + T + 5
+    g = gen(T)
+    qnw, knw = (w.to(DEV) for w in norm_weights(g))
+    pr = proj_rows(g, T, hq, hkv)
+    prd = pr.proj.to(DEV)
+    qg_d = prd[:, : hq * 2 * D]
+    k_d = prd[:, hq * 2 * D: hq * 2 * D + hkv * D]
+    v_d = prd[:, hq * 2 * D + hkv * D: hq * 2 * D + 2 * hkv * D]
+    inv = O.rope_inv_freq(1e7, 64).to(DEV)
+    kc_a = torch.zeros(hkv, max_len, D, dtype=BF, device=DEV)
+    vc_a, kc_b, vc_b = kc_a.clone(), kc_a.clone(), kc_a.clone()
+    q_a = torch.empty(T, hq * D, dtype=BF, device=DEV)
+    q_b = torch.empty_like(q_a)
+    C.attn_prep_chunk(qg_d, k_d, v_d, qnw, knw, inv, torch.tensor([pos], dtype=torch.int32,
+                      device=DEV), q_a, kc_a, vc_a, 1e-6)
+    for t0 in range(0, T, 8):
+        t1 = min(T, t0 + 8)
+        C.attn_prep(qg_d[t0:t1], k_d[t0:t1], v_d[t0:t1], qnw, knw, inv,
+                    torch.tensor([pos + t0], dtype=torch.int32, device=DEV), q_b[t0:t1], kc_b,
+                    vc_b, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(q_a.view(torch.int16), q_b.view(torch.int16))
+    assert torch.equal(kc_a.view(torch.int16), kc_b.view(torch.int16))
+    assert torch.equal(vc_a.view(torch.int16), vc_b.view(torch.int16))
