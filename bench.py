@@ -541,6 +541,26 @@ def bench_prefill(torch, C, steps: int, warmup: int) -> dict:
         "us_attention": round(ms_attn * 1e3, 2), "us_prep_plus_attention": round(ms_full * 1e3, 2),
         "GFLOP": round(flops / 1e9, 2), "TFLOPs": round(tflops, 1),
         "mfma_frac_of_2500_TFLOPs_bf16_dense": round(tflops / 2500.0, 4)}
+
+    # the same chunk over an fp8 cache (codes of the bf16 cache at scale 1/16): attn_prep_fp8
+    # writes the chunk's codes, attn_prefill_fp8 converts each tile once in LDS
+    ks = vs = 1.0 / 16
+    kc8 = torch.empty(HKV, L, D, dtype=torch.float8_e4m3fn, device=dev)
+    vc8 = torch.empty_like(kc8)
+    kc8.copy_((kc.float() * 16).clamp(-448, 448).to(torch.float8_e4m3fn))
+    vc8.copy_((vc.float() * 16).clamp(-448, 448).to(torch.float8_e4m3fn))
+    C.attn_prep_fp8(qgT, kT, vT, qnw, knw, inv, posT, qT, kc8, vc8, 1e-6, ks, vs)
+    ms8 = time_fn_graph(torch, lambda: C.attn_prefill_fp8(qT, kc8, vc8, posT, qgT, outT, ks, vs),
+                        steps, warmup)
+
+    def full8():
+        C.attn_prep_fp8(qgT, kT, vT, qnw, knw, inv, posT, qT, kc8, vc8, 1e-6, ks, vs)
+        C.attn_prefill_fp8(qT, kc8, vc8, posT, qgT, outT, ks, vs)
+    ms8_full = time_fn_graph(torch, full8, steps, warmup)
+    tf8 = flops / (ms8 * 1e-3) / 1e12
+    res["cfg5_prefill_fp8kv"] = {
+        "us_attention": round(ms8 * 1e3, 2), "us_prep_plus_attention": round(ms8_full * 1e3, 2),
+        "TFLOPs": round(tf8, 1), "mfma_frac_of_2500_TFLOPs_bf16_dense": round(tf8 / 2500.0, 4)}
     return res
 
 

@@ -122,6 +122,15 @@ hipError_t qe_attn_decode_fp8(const void* q, const void* kc8, const void* vc8, c
                               long ldo, int n, int Hq, int Hkv, int max_len, int NS, float scale,
                               float k_scale, float v_scale, hipStream_t stream);
 
+/* qe_attn_prefill over the fp8 cache: the same attention on the dequantized values (k_scale
+ * scales every score, v_scale the attention output before its bf16 rounding). With scales of 1
+ * it equals qe_attn_prefill on the dequantized cache bit for bit. Valid as qe_attn_prefill, plus
+ * k_scale, v_scale positive and finite. */
+hipError_t qe_attn_prefill_fp8(const void* q, const void* kc8, const void* vc8, const int* pos,
+                               const void* qg, long ldp, void* out, long ldo, int T, int Hq,
+                               int Hkv, int max_len, float scale, float k_scale, float v_scale,
+                               hipStream_t stream);
+
 /* First half of qe_attn_decode_fp8 (the partials are not yet multiplied by v_scale). */
 hipError_t qe_attn_decode_fp8_partials(const void* q, const void* kc8, const void* vc8,
                                        const int* pos, float* part_o, float* part_ml, int n,

@@ -26,6 +26,7 @@ SIGNATURES = {
     "qe_attn_decode_partials": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P]),
     "qe_attn_decode_combine": (_I, [_P, _P, _P, _P, _L, _P, _L, _I, _I, _I, _I, _P]),
     "qe_attn_prefill": (_I, [_P, _P, _P, _P, _P, _L, _P, _L, _I, _I, _I, _I, _F, _P]),
+    "qe_attn_prefill_fp8": (_I, [_P, _P, _P, _P, _P, _L, _P, _L, _I, _I, _I, _I, _F, _F, _F, _P]),
     "qe_attn_prep_decode": (_I, [_P, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _I, _I,
                                  _I, _I, _I, _I, _F, _F, _P]),
     "qe_attn_split_size": (_I, [_I, _I]),
@@ -125,6 +126,13 @@ def prefill(q, kc, vc, pos, qg, ldp, out, ldo, T, hq, hkv, max_len, scale=1.0 / 
             stream=None) -> int:
     return load().qe_attn_prefill(_ptr(q), _ptr(kc), _ptr(vc), _ptr(pos), _ptr(qg), ldp, _ptr(out),
                                   ldo, T, hq, hkv, max_len, scale, _stream(stream))
+
+
+def prefill_fp8(q, kc8, vc8, pos, qg, ldp, out, ldo, T, hq, hkv, max_len, k_scale, v_scale,
+                scale=1.0 / 16, stream=None) -> int:
+    return load().qe_attn_prefill_fp8(_ptr(q), _ptr(kc8), _ptr(vc8), _ptr(pos), _ptr(qg), ldp,
+                                      _ptr(out), ldo, T, hq, hkv, max_len, scale, k_scale, v_scale,
+                                      _stream(stream))
 
 
 def split_size(L: int, ns: int) -> int:

@@ -101,11 +101,72 @@ __device__ __forceinline__ void run_tiles(int j0, int j1, int Lwave, u32x4_t* ld
   }
 }
 
+// ---- fp8 KV cache (E4M3FN codes, 256-byte rows). Tiles arrive in a STAGES-deep fp8 ring by LDS
+// DMA (each wave fetches its 4 rows of K and of V: one 1 KB instruction each). At its turn a tile
+// is converted once by the 8 waves into a double-buffered bf16 K/V tile (the swizzled layouts of
+// the bf16 path: every E4M3 value is a bf16 value, so the conversion is exact), and the bf16 tile
+// math runs on it unchanged. The fp8 ring and the bf16 pair take 64 KB each.
+constexpr int TILE8_U4 = BN * ROW_CHUNKS / 2;   // 16-byte slots per fp8 K (or V) tile: 512
+constexpr int STAGE8_U4 = 2 * TILE8_U4;         // fp8 K tile then V tile (16 KB)
+constexpr int LOADS_PER_TILE8 = 2;              // one K and one V instruction per wave
+static_assert(STAGES * STAGE8_U4 + 2 * STAGE_U4 == STAGES * STAGE_U4, "fp8 ring + bf16 pair");
+
+__device__ __forceinline__ void issue_tile8(u32x4_t* stage, __amdgpu_buffer_rsrc_t krs,
+                                            __amdgpu_buffer_rsrc_t vrs, int p0, int w, int lane) {
+  const int r = LOAD_ROWS * w + (lane >> 4);  // lane i: row 4w + i/16, 16-byte chunk i % 16
+  buffer_load16_to_lds<PF_CPOL>(krs, (uint32_t)(p0 + r) * HD + (lane & 15) * 16,
+                                stage + LOAD_ROWS * w * (ROW_CHUNKS / 2));
+  buffer_load16_to_lds<PF_CPOL>(vrs, (uint32_t)(p0 + r) * HD + (lane & 15) * 16,
+                                stage + TILE8_U4 + LOAD_ROWS * w * (ROW_CHUNKS / 2));
+}
+
+// Thread i of the workgroup converts the 16 codes of fp8 chunk i (row i/16, dims 16(i%16) ..) of
+// the K and the V tile into two bf16 chunks each, at their swizzled bf16 slots.
+__device__ __forceinline__ void convert_tile8(const u32x4_t* stage, u32x4_t* bf) {
+  const int i = threadIdx.x, r = i >> 4, q = (i & 15) * 2;
+  const u32x4_t kk = stage[i], vv = stage[TILE8_U4 + i];
+  bf[tile::k_slot(r, q)] = fp8x8_to_bf16x8(u32x2_t{kk[0], kk[1]});
+  bf[tile::k_slot(r, q + 1)] = fp8x8_to_bf16x8(u32x2_t{kk[2], kk[3]});
+  bf[TILE_U4 + r * ROW_CHUNKS + (q ^ tile::v_swz(r))] = fp8x8_to_bf16x8(u32x2_t{vv[0], vv[1]});
+  bf[TILE_U4 + r * ROW_CHUNKS + ((q + 1) ^ tile::v_swz(r))] = fp8x8_to_bf16x8(u32x2_t{vv[2], vv[3]});
+}
+
+// run_tiles for the fp8 cache: iteration j converts tile j into bf16 pair j % 2 (whose previous
+// tile, j-2, every wave finished before iteration j-1's barrier), then computes it.
+template <bool SPLIT, bool MASK>
+__device__ __forceinline__ void run_tiles8(int j0, int j1, int Lwave, u32x4_t* lds,
+                                           __amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
+                                           int w, int lane, int c, int g4,
+                                           const bf16x8_t (&qb)[NT][8], const int (&Lcol)[NT],
+                                           float scale_log2, WaveState& st) {
+  u32x4_t* bfp = lds + STAGES * STAGE8_U4;
+  for (int j = j0; j < j1; ++j) {
+    const int p0 = j * BN;
+    vmcnt_wait<LOADS_PER_TILE8 * (AHEAD - 1)>();  // this wave's loads of tile j are done
+    __syncthreads();  // ... and every wave's; tile j-1's fp8 stage and pair j % 2 are free
+    issue_tile8(lds + ((j + AHEAD) % STAGES) * STAGE8_U4, krs, vrs, p0 + AHEAD * BN, w, lane);
+    u32x4_t* bf = bfp + (j & 1) * STAGE_U4;
+    convert_tile8(lds + (j % STAGES) * STAGE8_U4, bf);
+    lds_barrier();  // the bf16 tile is complete
+    if (p0 >= Lwave) continue;
+    f32x4_t sacc[NT][2];
+    tile::qk_tile<NT>(bf, qb, c, g4, sacc);
+    u32x4_t pb_hi[NT], pb_lo[NT];
+    tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc, pb_hi,
+                                        pb_lo);
+    tile::pv_tile_tr<NT, SPLIT>(bf + TILE_U4, lane, g4, pb_hi, pb_lo, st.acc);
+  }
+}
+
+// KV8: kc/vc hold fp8 codes (one byte per value); v_scale multiplies O / l before its bf16
+// rounding (exactly 1 for the bf16 cache).
+template <bool KV8>
 __global__ void __launch_bounds__(WAVES * WAVE)
-attn_prefill_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
-                    const __bf16* __restrict__ vc, const int* __restrict__ pos_ptr,
+attn_prefill_kernel(const __bf16* __restrict__ q, const void* __restrict__ kc,
+                    const void* __restrict__ vc, const int* __restrict__ pos_ptr,
                     const __bf16* __restrict__ qg, long ldp, __bf16* __restrict__ out, long ldo,
-                    int T, int Hq, int Hkv, int max_len, float scale_log2, int xcd_split) {
+                    int T, int Hq, int Hkv, int max_len, float scale_log2, float v_scale,
+                    int xcd_split) {
   const int grp = Hq / Hkv;
   const int nblk = (T + BQ - 1) / BQ;
   int blk, h;
@@ -157,10 +218,11 @@ attn_prefill_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
   const int ntiles = Lwg > 0 ? (Lwg + BN - 1) / BN : 0;
   const bool split = Lmin < SPLIT_BELOW;
 
-  const size_t head_off = (size_t)g * max_len * HD;
-  const uint32_t bytes = (uint32_t)max(Lwg, 0) * (uint32_t)(HD * 2);  // past Lwg reads 0
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kc + head_off, bytes);
-  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vc + head_off, bytes);
+  constexpr int ELEM = KV8 ? 1 : 2;  // bytes per cache value
+  const size_t head_off = (size_t)g * max_len * HD * ELEM;  // bytes
+  const uint32_t bytes = (uint32_t)max(Lwg, 0) * (uint32_t)(HD * ELEM);  // past Lwg reads 0
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(static_cast<const char*>(kc) + head_off, bytes);
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(static_cast<const char*>(vc) + head_off, bytes);
 
   WaveState st;
 #pragma unroll
@@ -173,16 +235,28 @@ attn_prefill_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
 
   // Ring of STAGES tiles, AHEAD in flight. One barrier per tile: after the barrier of tile j every
   // wave has finished tile j-1, whose stage is the one refilled with tile j+AHEAD.
-#pragma unroll
-  for (int a = 0; a < AHEAD; ++a) issue_tile(lds + a * STAGE_U4, krs, vrs, a * BN, w, lane);
   // Tiles below jm need no per-position mask (every real row of the wave attends them fully).
   const int jm = min(ntiles, max(Lmin, 0) / BN);
+  if constexpr (KV8) {
+#pragma unroll
+    for (int a = 0; a < AHEAD; ++a) issue_tile8(lds + a * STAGE8_U4, krs, vrs, a * BN, w, lane);
+    if (split) {
+      run_tiles8<true, false>(0, jm, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol, scale_log2, st);
+      run_tiles8<true, true>(jm, ntiles, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol, scale_log2, st);
+    } else {
+      run_tiles8<false, false>(0, jm, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol, scale_log2, st);
+      run_tiles8<false, true>(jm, ntiles, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol, scale_log2, st);
+    }
+  } else {
+#pragma unroll
+  for (int a = 0; a < AHEAD; ++a) issue_tile(lds + a * STAGE_U4, krs, vrs, a * BN, w, lane);
   if (split) {
     run_tiles<true, false>(0, jm, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol, scale_log2, st);
     run_tiles<true, true>(jm, ntiles, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol, scale_log2, st);
   } else {
     run_tiles<false, false>(0, jm, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol, scale_log2, st);
     run_tiles<false, true>(jm, ntiles, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol, scale_log2, st);
+  }
   }
   vmcnt_wait<0>();  // no LDS DMA may still target this workgroup's LDS when it exits
 
@@ -201,8 +275,8 @@ attn_prefill_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
       u32x2_t ob;
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
-        const float o0 = round_bf16(st.acc[ct][i][2 * k] / L);
-        const float o1 = round_bf16(st.acc[ct][i][2 * k + 1] / L);
+        const float o0 = round_bf16((st.acc[ct][i][2 * k] / L) * v_scale);
+        const float o1 = round_bf16((st.acc[ct][i][2 * k + 1] / L) * v_scale);
         const float s0 = round_bf16(sigmoid_f32(lo_bf16(gb[k])));
         const float s1 = round_bf16(sigmoid_f32(hi_bf16(gb[k])));
         ob[k] = pack_bf16x2(o0 * s0, o1 * s1);
@@ -217,16 +291,17 @@ attn_prefill_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
 
 using namespace qe;
 
-extern "C" hipError_t qe_attn_prefill(const void* q, const void* kc, const void* vc,
-                                      const int* pos, const void* qg, long ldp, void* out,
-                                      long ldo, int T, int Hq, int Hkv, int max_len, float scale,
-                                      hipStream_t stream) {
+static hipError_t launch_prefill(const void* q, const void* kc, const void* vc, const int* pos,
+                                 const void* qg, long ldp, void* out, long ldo, int T, int Hq,
+                                 int Hkv, int max_len, float scale, bool kv8, float k_scale,
+                                 float v_scale, hipStream_t stream) {
   auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   if (T < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || max_len < 1 || !pos ||
       (long)((T + prefill::BQ - 1) / prefill::BQ) * Hq > 0x7fffffffL)
     return hipErrorInvalidValue;
   if (!a16(q) || !a16(kc) || !a16(vc) || !a16(qg) || !a16(out) || ldp % 8 != 0 || ldo % 8 != 0)
     return hipErrorInvalidValue;
+  // byte offsets of the tiles loaded past the last attended row fit the 32-bit buffer range
   if ((unsigned long long)(max_len + (prefill::AHEAD + 2) * prefill::BN) * HD * 2 >= (1ull << 32))
     return hipErrorInvalidValue;
   const int nblk = (T + prefill::BQ - 1) / prefill::BQ;
@@ -235,10 +310,35 @@ extern "C" hipError_t qe_attn_prefill(const void* q, const void* kc, const void*
   const int per_head = prefill::XCDS % Hkv == 0 ? prefill::XCDS / Hkv : 0;
   const int xcd_split =
       per_head > 0 && (nblk * (Hq / Hkv)) % per_head == 0 ? per_head : 0;
-  prefill::attn_prefill_kernel<<<dim3(nblk * Hq), dim3(prefill::WAVES * WAVE), 0, stream>>>(
-      static_cast<const __bf16*>(q), static_cast<const __bf16*>(kc),
-      static_cast<const __bf16*>(vc), pos, static_cast<const __bf16*>(qg), ldp,
-      static_cast<__bf16*>(out), ldo, T, Hq, Hkv, max_len, scale * 1.4426950408889634f,
-      xcd_split);
+  const float scale_log2 = scale * 1.4426950408889634f * k_scale;
+  const dim3 grid(nblk * Hq), block(prefill::WAVES * WAVE);
+  const auto* Q = static_cast<const __bf16*>(q);
+  const auto* QG = static_cast<const __bf16*>(qg);
+  auto* O = static_cast<__bf16*>(out);
+  if (kv8)
+    prefill::attn_prefill_kernel<true><<<grid, block, 0, stream>>>(
+        Q, kc, vc, pos, QG, ldp, O, ldo, T, Hq, Hkv, max_len, scale_log2, v_scale, xcd_split);
+  else
+    prefill::attn_prefill_kernel<false><<<grid, block, 0, stream>>>(
+        Q, kc, vc, pos, QG, ldp, O, ldo, T, Hq, Hkv, max_len, scale_log2, 1.f, xcd_split);
   return hipGetLastError();
+}
+
+extern "C" hipError_t qe_attn_prefill(const void* q, const void* kc, const void* vc,
+                                      const int* pos, const void* qg, long ldp, void* out,
+                                      long ldo, int T, int Hq, int Hkv, int max_len, float scale,
+                                      hipStream_t stream) {
+  return launch_prefill(q, kc, vc, pos, qg, ldp, out, ldo, T, Hq, Hkv, max_len, scale, false, 1.f,
+                        1.f, stream);
+}
+
+extern "C" hipError_t qe_attn_prefill_fp8(const void* q, const void* kc8, const void* vc8,
+                                          const int* pos, const void* qg, long ldp, void* out,
+                                          long ldo, int T, int Hq, int Hkv, int max_len,
+                                          float scale, float k_scale, float v_scale,
+                                          hipStream_t stream) {
+  if (!(k_scale > 0.f) || !(v_scale > 0.f) || k_scale == INFINITY || v_scale == INFINITY)
+    return hipErrorInvalidValue;
+  return launch_prefill(q, kc8, vc8, pos, qg, ldp, out, ldo, T, Hq, Hkv, max_len, scale, true,
+                        k_scale, v_scale, stream);
 }

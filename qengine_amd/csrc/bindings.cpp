@@ -299,7 +299,8 @@ void attn_prep_fp8(torch::Tensor qg, torch::Tensor k, torch::Tensor v, torch::Te
                    torch::Tensor knw, torch::Tensor inv_freq, torch::Tensor pos, torch::Tensor q_out,
                    torch::Tensor kc8, torch::Tensor vc8, double eps, double k_scale,
                    double v_scale) {
-  const auto a = parse_prep(qg, k, v, qnw, knw, inv_freq, pos, q_out, kc8, vc8, true, 8, true);
+  // no reference counterpart: any row count, so it also fills the fp8 cache for prefill chunks
+  const auto a = parse_prep(qg, k, v, qnw, knw, inv_freq, pos, q_out, kc8, vc8, true, 65535, true);
   kv_scales(k_scale, v_scale);
   const c10::DeviceGuard guard(qg.device());
   raise_on(qe_attn_prep_fp8(qg.data_ptr(), k.data_ptr(), v.data_ptr(), a.ldp, qnw.data_ptr(),
@@ -308,6 +309,32 @@ void attn_prep_fp8(torch::Tensor qg, torch::Tensor k, torch::Tensor v, torch::Te
                             a.max_len, a.rd, (float)eps, (float)k_scale, (float)v_scale,
                             stream_of(qg)),
            "qe_attn_prep_fp8");
+}
+
+// attn_prefill over the fp8 cache (kc8/vc8 [Hkv, max_len, 256] E4M3FN codes).
+void attn_prefill_fp8(torch::Tensor q, torch::Tensor kc8, torch::Tensor vc8, torch::Tensor pos,
+                      torch::Tensor qg, torch::Tensor out, double k_scale, double v_scale) {
+  auto Qr = rows(q, BF, "q", true), QG = rows(qg, BF, "qg", true), O = rows(out, BF, "out", true);
+  chk_kv8(kc8, "kc8", true);
+  chk_kv8(vc8, "vc8", true);
+  chk_pos(pos, true);
+  kv_scales(k_scale, v_scale);
+  chk16(q, Qr.ld, "q");
+  chk16(qg, QG.ld, "qg");
+  chk16(out, O.ld, "out");
+  chk16(kc8, HD, "kc8");
+  chk16(vc8, HD, "vc8");
+  TORCH_CHECK(kc8.dim() == 3 && kc8.size(2) == HD && vc8.sizes() == kc8.sizes(),
+              "kc8/vc8 must be [Hkv, max_len, 256] with equal sizes");
+  const int T = Qr.n, Hq = Qr.w / HD, Hkv = kc8.size(0), max_len = kc8.size(1);
+  TORCH_CHECK(Hq >= 1 && Qr.ld == Qr.w && QG.n == T && O.n == T && Hq % Hkv == 0,
+              "q rows must be contiguous, rows must agree and Hq % Hkv == 0");
+  TORCH_CHECK(O.w == (long)Hq * HD && QG.w >= (long)Hq * 2 * HD, "out width Hq*256; qg width Hq*512");
+  const c10::DeviceGuard guard(q.device());
+  raise_on(qe_attn_prefill_fp8(q.data_ptr(), kc8.data_ptr(), vc8.data_ptr(), pos.data_ptr<int>(),
+                               qg.data_ptr(), QG.ld, out.data_ptr(), O.ld, T, Hq, Hkv, max_len,
+                               1.0f / 16.0f, (float)k_scale, (float)v_scale, stream_of(q)),
+           "qe_attn_prefill_fp8");
 }
 
 void attn_decode_fp8(torch::Tensor q, torch::Tensor kc8, torch::Tensor vc8, torch::Tensor pos,
@@ -633,6 +660,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("attn_prep_fp8", &attn_prep_fp8,
         "attn_prep writing the fp8 KV cache (qg, k, v, qnw, knw, inv_freq, pos, q_out, kc8, vc8, "
         "eps, k_scale, v_scale)");
+  m.def("attn_prefill_fp8", &attn_prefill_fp8,
+        "attn_prefill over the fp8 cache (q, kc8, vc8, pos, qg, out, k_scale, v_scale)");
   m.def("attn_decode_fp8", &attn_decode_fp8,
         "attn_decode over the fp8 KV cache (q, kc8, vc8, pos, qg, part_o, part_ml, out, k_scale, "
         "v_scale)");

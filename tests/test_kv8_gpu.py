@@ -151,3 +151,70 @@ def test_fp8_wide_verify_vs_oracle_and_rows(native, ks, vs):
     for t in range(n):
         o1 = run_fp8(native, case.q[t:t + 1], case.qg[t:t + 1], kc8, vc8, case.pos + t, 64, ks, vs)
         assert torch.equal(o1[0], out[t]), t
+
+
+def run_prefill(C, q, qg, kc, vc, pos, fp8=False, ks=1.0, vs=1.0):
+    T, hq = q.shape[0], q.shape[1] // D
+    out = torch.empty(T, hq * D, dtype=BF, device=DEV)
+    p = torch.tensor([pos], dtype=torch.int32, device=DEV)
+    if fp8:
+        C.attn_prefill_fp8(q.to(DEV), kc.to(DEV), vc.to(DEV), p, qg.to(DEV), out, ks, vs)
+    else:
+        C.attn_prefill(q.to(DEV), kc.to(DEV), vc.to(DEV), p, qg.to(DEV), out)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+@pytest.mark.parametrize("hq,hkv,T,pos", [(24, 4, 200, 300), (8, 2, 129, 0), (24, 4, 64, 2000),
+                                          (16, 1, 300, 700)])
+def test_prefill_fp8_scale_one_equals_bf16(native, hq, hkv, T, pos):
+    """Chunked prefill over the fp8 cache with scales of 1 equals attn_prefill over the
+    dequantized bf16 cache bit for bit (short rows included: they take the hi + lo P split)."""
+    case = decode_case(seed=T + pos, hq=hq, hkv=hkv, pos=pos, n=T, max_len=pos + T + 9)
+    kc8, vc8 = quantize_cache(case.kc, 1.0), quantize_cache(case.vc, 1.0)
+    kd = K8.dequantize(kc8.view(torch.uint8), 1.0).to(BF)
+    vd = K8.dequantize(vc8.view(torch.uint8), 1.0).to(BF)
+    a = run_prefill(native, case.q, case.qg, kc8, vc8, pos, fp8=True)
+    b = run_prefill(native, case.q, case.qg, kd, vd, pos)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("ks,vs", [(0.5, 0.25), (0.037, 0.011), (3.0, 2.0)])
+def test_prefill_fp8_vs_oracle(native, ks, vs):
+    case = decode_case(seed=int(ks * 1000), hq=24, hkv=4, pos=1000, n=300, max_len=1400)
+    kc8, vc8 = quantize_cache(case.kc, ks), quantize_cache(case.vc, vs)
+    out = run_prefill(native, case.q, case.qg, kc8, vc8, case.pos, fp8=True, ks=ks, vs=vs)
+    kd = K8.dequantize(kc8.view(torch.uint8), ks)
+    vd = K8.dequantize(vc8.view(torch.uint8), vs)
+    ref = O.attn_prefill(case.q, kd, vd, case.pos, case.qg, case.hq)
+    ok, mx, mean = attn_close(out, ref)
+    assert ok, (mx, mean)
+
+
+def test_prep_fp8_chunk_equals_eight_row_preps(native):
+    """attn_prep_fp8 over 40 rows (8 rows per workgroup) writes the same q and codes as calls of
+    8 rows."""
+    from attn_cases import gen, norm_weights, proj_rows
+    C = native
+    hq, hkv, T, pos, max_len, ks, vs = 24, 4, 40, 100, 160, 0.5, 0.25
+    g = gen(77)
+    qnw, knw = (w.to(DEV) for w in norm_weights(g))
+    prd = proj_rows(g, T, hq, hkv).proj.to(DEV)
+    qg = prd[:, : hq * 2 * D]
+    k = prd[:, hq * 2 * D: hq * 2 * D + hkv * D]
+    v = prd[:, hq * 2 * D + hkv * D: hq * 2 * D + 2 * hkv * D]
+    inv = O.rope_inv_freq(1e7, 64).to(DEV)
+    kc_a = torch.zeros(hkv, max_len, D, dtype=torch.uint8, device=DEV).view(F8)
+    vc_a, kc_b, vc_b = kc_a.clone(), kc_a.clone(), kc_a.clone()
+    q_a = torch.empty(T, hq * D, dtype=BF, device=DEV)
+    q_b = torch.empty_like(q_a)
+    C.attn_prep_fp8(qg, k, v, qnw, knw, inv, torch.tensor([pos], dtype=torch.int32, device=DEV),
+                    q_a, kc_a, vc_a, 1e-6, ks, vs)
+    for t0 in range(0, T, 8):
+        C.attn_prep_fp8(qg[t0:t0 + 8], k[t0:t0 + 8], v[t0:t0 + 8], qnw, knw, inv,
+                        torch.tensor([pos + t0], dtype=torch.int32, device=DEV), q_b[t0:t0 + 8],
+                        kc_b, vc_b, 1e-6, ks, vs)
+    torch.cuda.synchronize()
+    assert torch.equal(q_a.view(torch.int16), q_b.view(torch.int16))
+    assert torch.equal(kc_a.view(torch.uint8), kc_b.view(torch.uint8))
+    assert torch.equal(vc_a.view(torch.uint8), vc_b.view(torch.uint8))
