@@ -91,6 +91,31 @@ def test_capi_decode_rejects(capi, kw, why):
     assert r == INVALID, why
 
 
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("kw,why", [
+    (dict(T=0), "no rows"), (dict(hq=25), "Hq % Hkv"), (dict(hkv=0), "no kv heads"),
+    (dict(max_len=0), "empty cache"), (dict(pos=None), "null pos"), (dict(q=A + 8), "q unaligned"),
+    (dict(ldp=12), "qg row stride not a multiple of 8"), (dict(max_len=1 << 23), "32-bit offsets"),
+])
+def test_capi_prefill_rejects(capi, fp8, kw, why):
+    """qe_attn_prefill / qe_attn_prefill_fp8 reject out-of-range arguments before any launch."""
+    a = dict(q=A, kc=A, vc=A, pos=A, qg=A, ldp=48 * D, out=A, ldo=24 * D, T=16, hq=24, hkv=4,
+             max_len=4096)
+    a.update(kw)
+    args = (a["q"], a["kc"], a["vc"], a["pos"], a["qg"], a["ldp"], a["out"], a["ldo"], a["T"],
+            a["hq"], a["hkv"], a["max_len"], 1.0 / 16)
+    lib = capi.load()
+    r = lib.qe_attn_prefill_fp8(*args, 1.0, 1.0, None) if fp8 else lib.qe_attn_prefill(*args, None)
+    assert r == INVALID, why
+
+
+@pytest.mark.parametrize("ks,vs", [(0.0, 1.0), (1.0, -1.0), (float("inf"), 1.0), (1.0, float("nan"))])
+def test_capi_prefill_fp8_rejects_scales(capi, ks, vs):
+    r = capi.load().qe_attn_prefill_fp8(A, A, A, A, A, 48 * D, A, 24 * D, 16, 24, 4, 4096, 1.0 / 16,
+                                        ks, vs, None)
+    assert r == INVALID
+
+
 @pytest.mark.parametrize("kw,why", [
     (dict(n=0), "no rows"), (dict(rd=3), "odd rotary dims"), (dict(rd=258), "rd > 256"),
     (dict(max_len=0), "empty cache"), (dict(hkv=0), "no kv heads"), (dict(qg=None), "null"),
