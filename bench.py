@@ -124,8 +124,8 @@ def bench_length_fp8(torch, C, qa, L: int, steps: int, warmup: int) -> dict:
     sets = [LayerSet8(torch, C, L, ns, gen) for _ in range(nsets)]
     full = [capture(torch, s.decode_all) for s in sets]
     part = [capture(torch, s.partials_all) for s in sets]
-    us_layer = time_graphs(torch, full, steps, warmup) * 1e3 / LAYERS
-    us_part = time_graphs(torch, part, steps, warmup) * 1e3 / LAYERS
+    us_layer = time_graphs(torch, full, steps, warmup).median * 1e3 / LAYERS
+    us_part = time_graphs(torch, part, steps, warmup).median * 1e3 / LAYERS
     b_layer = 2048 * L + 36864
     b_part = 2048 * L + 12288
     del sets, full, part
@@ -149,50 +149,126 @@ def capture(torch, fn):
     return g
 
 
-def time_graphs(torch, graphs, steps: int, warmup: int) -> float:
-    """Replays graphs round-robin; returns ms per replay over exactly `steps` timed replays.
-    Events are recorded on the current stream, the one the graphs' kernels run on."""
-    for i in range(warmup):
+MIN_WARMUP_REPLAYS = 30  # the reference's time_graph warms each graph up 30 times
+
+
+class Timing:
+    """Per-replay graph timings in ms: ``mean`` over the bracketed run of exactly ``steps``
+    replays, and the median / min / max of the individual replays (HIP events between replays on
+    the stream the graphs run on)."""
+
+    def __init__(self, mean: float, per: list):
+        per = sorted(per)
+        self.mean, self.median, self.min, self.max = mean, statistics.median(per), per[0], per[-1]
+
+    def us(self, div: int = 1) -> dict:
+        return {k: round(getattr(self, k) * 1e3 / div, 3) for k in ("median", "mean", "min", "max")}
+
+
+def time_graphs(torch, graphs, steps: int, warmup: int) -> Timing:
+    """The reference's graph timing (bench/engine/micro_kernels.py:16-32): at least 30 warm-up
+    replays, then ``steps`` timed replays (graphs round-robin), each bracketed by events on the
+    current stream, the one the graphs' kernels run on."""
+    for i in range(max(warmup, MIN_WARMUP_REPLAYS)):
         graphs[i % len(graphs)].replay()
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record()
     for i in range(steps):
         graphs[i % len(graphs)].replay()
-    e1.record()
+        ev[i + 1].record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    return Timing(ev[0].elapsed_time(ev[steps]) / steps, per)
+
+
+def warm_device(torch, seconds: float = 1.0) -> float:
+    """At least ``seconds`` of streaming reads before the first timed graph, so clocks and HBM
+    have left idle (the reference warms up before timing: micro_kernels.py:16-32)."""
+    import qengine_amd.capi as capi
+    buf = torch.ones(256 * 2 ** 20 // 4, dtype=torch.int32, device="cuda")
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(50):
+            capi.hbm_read_probe(buf, buf.numel() * 4, sink)
+        torch.cuda.synchronize()
+    del buf
+    return time.perf_counter() - t0
 
 
 def bench_length(torch, C, qa, L: int, steps: int, warmup: int, ns: int | None):
+    """Layer-calls at KV length L (16 per graph on distinct caches, >= 512 MB in rotation): the
+    whole op, its partials kernel alone, and the two ceilings measured the same way: the
+    streaming probe on the partials grid (the K/V bytes, no arithmetic) and an empty launch."""
+    import qengine_amd.capi as capi
     ns = ns or qa.default_splits(L, HKV)
     nsets = max(1, math.ceil(ROTATE_BYTES / (LAYERS * L * 4096)))
     gen = torch.Generator(device="cuda").manual_seed(L)
     sets = [LayerSet(torch, C, L, ns, gen) for _ in range(nsets)]
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def probe_all(s):
+        for k, v in zip(s.kc, s.vc):
+            capi.kv_stream_probe(k, v, L, HKV, L, ns, sink)
     full = [capture(torch, s.decode_all) for s in sets]
     part = [capture(torch, s.partials_all) for s in sets]
-    ms_step = time_graphs(torch, full, steps, warmup)
-    ms_part = time_graphs(torch, part, steps, warmup)
-    us_layer = ms_step * 1e3 / LAYERS
-    us_part = ms_part * 1e3 / LAYERS
+    probe = [capture(torch, lambda s=s: probe_all(s)) for s in sets]
+    t_full = time_graphs(torch, full, steps, warmup)
+    t_part = time_graphs(torch, part, steps, warmup)
+    t_probe = time_graphs(torch, probe, steps, warmup)
+    us_layer = t_full.median * 1e3 / LAYERS
+    us_part = t_part.median * 1e3 / LAYERS
+    us_probe = t_probe.median * 1e3 / LAYERS
     res = {
         "L": L, "NS": ns, "split_size": qa.split_size(L, ns), "kv_rotation_MB":
             round(nsets * LAYERS * L * 4096 / 2 ** 20, 1),
-        "ms_per_step": ms_step, "us_per_layer": us_layer,
+        "ms_per_step": t_full.mean, "ms_per_step_median": t_full.median,
+        "us_per_layer": us_layer, "us_per_layer_stats": t_full.us(LAYERS),
         "GBps": alg_bytes_layer(L) / (us_layer * 1e3),
-        "partials_us": us_part, "partials_GBps": alg_bytes_partials(L) / (us_part * 1e3),
+        "partials_us": us_part, "partials_us_stats": t_part.us(LAYERS),
+        "partials_GBps": alg_bytes_partials(L) / (us_part * 1e3),
+        "partials_us_mean": t_part.mean * 1e3 / LAYERS,
+        "kv_stream_probe_us": us_probe,
     }
     res["frac"] = res["GBps"] / HBM_PEAK_GBS
     res["partials_frac"] = res["partials_GBps"] / HBM_PEAK_GBS
-    del sets, full, part
+    del sets, full, part, probe
     torch.cuda.empty_cache()
     return res
 
 
+def ceiling(sweep, node_us: float) -> dict:
+    """What any design can reach on this box, per KV length, in µs per layer-call: the streaming
+    probe on the partials grid is the floor of one launch that reads the K/V bytes; adding one
+    empty graph node gives the floor of a two-launch layer-call (partials + combine); the
+    BASELINE target is 75% of 8 TB/s on the algorithmic bytes."""
+    out = {"graph_node_us": round(node_us, 3), "per_L": {}}
+    for r in sweep:
+        L = r["L"]
+        out["per_L"][str(L)] = {
+            "kv_stream_probe_us": round(r["kv_stream_probe_us"], 3),
+            "one_launch_floor_us": round(r["kv_stream_probe_us"], 3),
+            "two_launch_floor_us": round(r["kv_stream_probe_us"] + node_us, 3),
+            "measured_us": round(r["us_per_layer"], 3),
+            "target_75pct_us": round(alg_bytes_layer(L) / (0.75 * HBM_PEAK_GBS * 1e3), 3)}
+    return out
+
+
+def launch_floor_us(torch, steps: int, warmup: int) -> float:
+    """µs per node of a graph of 16 empty launches: what every kernel in a graph pays."""
+    import qengine_amd.capi as capi
+
+    def run():
+        for _ in range(LAYERS):
+            capi.launch_probe()
+    return time_graphs(torch, [capture(torch, run)], steps, warmup).median * 1e3 / LAYERS
+
+
 def time_fn_graph(torch, fn, steps: int, warmup: int) -> float:
-    """ms per replay of a graph capturing fn()."""
-    return time_graphs(torch, [capture(torch, fn)], steps, warmup)
+    """ms per replay (median) of a graph capturing fn()."""
+    return time_graphs(torch, [capture(torch, fn)], steps, warmup).median
 
 
 def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
@@ -498,7 +574,7 @@ def bench_gdn(torch, C, steps: int, warmup: int) -> dict:
             for Ld in s:
                 call(Ld, n, prime)
         graphs = [capture(torch, lambda s=s: [call(Ld, n, ctl) for Ld in s]) for s in sets]
-        us = time_graphs(torch, graphs, steps, warmup) * 1e3 / nl
+        us = time_graphs(torch, graphs, steps, warmup).median * 1e3 / nl
         nb = gdn_alg_bytes(n, n)
         res[f"gdn_step_rows{n}"] = {"us": round(us, 3), "alg_bytes": nb,
                                     "GBps": round(nb / (us * 1e3), 1),
@@ -564,23 +640,64 @@ def bench_prefill(torch, C, steps: int, warmup: int) -> dict:
     return res
 
 
-def cpu_baseline(torch, L: int, reps: int = 5, warm: int = 2):
-    """The reference's PyTorch attention path (reference.py:263-272, restated op for op in
-    oracle/) timed on this host's CPU cores: one layer-call at KV length L."""
-    import oracle as O
-    torch.set_num_threads(os.cpu_count() or 1)
-    g = torch.Generator().manual_seed(L)
-    kc = torch.randn(HKV, L, D, generator=g).to(torch.bfloat16)
-    vc = torch.randn(HKV, L, D, generator=g).to(torch.bfloat16)
-    q = torch.randn(HQ, D, generator=g).to(torch.bfloat16)
-    gate = torch.randn(HQ * D, generator=g).to(torch.bfloat16)
+def _median_us(fn, reps: int, warm: int) -> float:
     ts = []
     for i in range(warm + reps):
         t0 = time.perf_counter()
-        O.attention_core(q, gate, kc, vc, L)
+        fn()
         if i >= warm:
             ts.append(time.perf_counter() - t0)
     return statistics.median(ts) * 1e6
+
+
+def cpu_baseline(torch, lengths=(1024, 4096, 16384, 32768, 131072), reps: int = 5,
+                 warm: int = 2) -> dict:
+    """The reference's PyTorch attention path (reference.py:252-280, restated op for op in
+    oracle/) timed on this host's CPU cores, per layer-call: one decode row at each KV length
+    (attention_core, which repeats K/V per GQA group in fp32 as the reference does), config 1 as
+    prep + decode at 1024, config 3 (5 causal rows at pos 4096, sequential attention_core calls as
+    reference.py:275-280 runs them), and config 5 timed on 64 evenly spaced rows of the 2048-row
+    chunk and extrapolated to 2048 rows (labelled). Medians of ``reps`` after ``warm``."""
+    import oracle as O
+    torch.set_num_threads(os.cpu_count() or 1)
+    res = {}
+    g = torch.Generator().manual_seed(7)
+    bf = torch.bfloat16
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=g) * scale).to(bf)
+    q, gate = rnd(HQ, D), rnd(HQ * D)
+    for L in lengths:
+        kc, vc = rnd(HKV, L, D), rnd(HKV, L, D)
+        r = reps if L < 131072 else 3
+        res[f"decode_{L // 1024}k"] = round(_median_us(lambda: O.attention_core(q, gate, kc, vc, L), r, warm if L < 131072 else 1), 1)
+        if L == 1024:
+            proj = rnd(1, HQ * 2 * D + 2 * HKV * D, scale=3.0)
+            qg1, k1, v1 = proj[:, :HQ * 2 * D], proj[:, HQ * 2 * D:HQ * 2 * D + HKV * D], proj[:, HQ * 2 * D + HKV * D:]
+            qnw, knw = rnd(D, scale=0.3), rnd(D, scale=0.3)
+            inv = O.rope_inv_freq(1e7, 64)
+
+            def cfg1():
+                qq = O.attn_prep(qg1, k1, v1, qnw, knw, inv, L - 1, kc, vc, 1e-6, HQ)
+                O.attention_core(qq[0].reshape(HQ, D), gate, kc, vc, L)
+            res["cfg1_prep_decode_1k"] = round(_median_us(cfg1, reps, warm), 1)
+        del kc, vc
+    L3, n3 = 4096 + 5, 5
+    kc, vc = rnd(HKV, L3, D), rnd(HKV, L3, D)
+    q5, qg5 = rnd(n3, HQ * D), rnd(n3, HQ * 2 * D)
+    res["cfg3_mtp_verify_5rows_4k"] = round(_median_us(
+        lambda: O.attn_decode(q5, kc, vc, 4096, qg5, HQ, grouped=False), reps, warm), 1)
+    T, pos0 = 2048, 2048
+    kc, vc = rnd(HKV, pos0 + T, D), rnd(HKV, pos0 + T, D)
+    rows = [round(i * (T - 1) / 63) for i in range(64)]
+
+    def cfg5_sample():
+        for t in rows:
+            O.attention_core(q, gate, kc, vc, pos0 + t + 1)
+    us64 = _median_us(cfg5_sample, 3, 1)
+    res["cfg5_prefill_2048_on_2048_extrapolated"] = round(us64 * T / len(rows), 1)
+    res["cfg5_sample"] = "64 evenly spaced rows of the 2048-row chunk, x 2048/64"
+    return res
 
 
 def cpu_model() -> str:
@@ -609,7 +726,8 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=MIN_WARMUP_REPLAYS,
+                    help="untimed replays before each timed graph (at least 30 are run)")
     ap.add_argument("--lengths", default="4096,16384,32768")
     ap.add_argument("--ns", type=int, default=0, help="split count (0 = default policy)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -670,12 +788,17 @@ def main():
     lengths = [int(x) for x in args.lengths.split(",") if x]
     if HEADLINE_L not in lengths:
         lengths.append(HEADLINE_L)
+    warm_s = warm_device(torch)
+    node_us = launch_floor_us(torch, args.steps, args.warmup)
+    print(f"# warm-up {warm_s:.2f} s; empty graph node {node_us:.2f} us", file=sys.stderr,
+          flush=True)
     sweep = []
     for L in lengths:
         r = bench_length(torch, C, qa, L, args.steps, args.warmup, args.ns or None)
         print(f"# L={L}: {r['us_per_layer']:.2f} us/layer-call, {r['GBps']:.0f} GB/s "
               f"({100 * r['frac']:.1f}%), partials {r['partials_us']:.2f} us "
-              f"({100 * r['partials_frac']:.1f}%)", file=sys.stderr, flush=True)
+              f"({100 * r['partials_frac']:.1f}%); stream probe {r['kv_stream_probe_us']:.2f} us",
+              file=sys.stderr, flush=True)
         sweep.append(r)
     head = next(r for r in sweep if r["L"] == HEADLINE_L)
     configs = None
@@ -686,12 +809,15 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        cpu_us = cpu_baseline(torch, HEADLINE_L)
-        cpu = {"value": cpu_us, "unit": "us/layer-call", "cores": torch.get_num_threads(),
-               "kind": "port",
-               "sample": f"oracle.attention_core (reference.py:263-272 restated in torch, CPU) "
-                         f"at KV {HEADLINE_L}, 1 layer-call, median of 5 after 2 warm-ups",
-               "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count()}
+        per = cpu_baseline(torch)
+        cpu = {"value": per[f"decode_{HEADLINE_L // 1024}k"], "unit": "us/layer-call",
+               "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"oracle.attention_core (reference.py:263-272 restated in torch, CPU), "
+                         f"1 layer-call at KV {HEADLINE_L}, median of 5 after 2 warm-ups; "
+                         f"per_config holds every length and configs 1, 3, 5 (5 extrapolated "
+                         f"from 64 rows)",
+               "per_config_us": per, "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count()}
+        print(f"# cpu baseline: {per}", file=sys.stderr, flush=True)
 
     line = {
         "metric": METRIC,
@@ -713,11 +839,13 @@ def main():
         "achieved_GBps": round(head["GBps"], 1),
         "hbm_frac": round(head["frac"], 4),
         "roofline": {"bound": "hbm", "kernel": "attn_partials_kernel",
-                     "achieved": round(head["partials_GBps"], 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(head["partials_frac"], 4),
+                     "achieved": round(alg_bytes_partials(HEADLINE_L) / (head["partials_us_mean"] * 1e3), 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(alg_bytes_partials(HEADLINE_L) / (head["partials_us_mean"] * 1e3) / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profiles(HEADLINE_L),
                      "alg_bytes_per_launch": alg_bytes_partials(HEADLINE_L),
-                     "avg_launch_us": round(head["partials_us"], 3)},
+                     "avg_launch_us": round(head["partials_us_mean"], 3)},
+        "ceiling": ceiling(sweep, node_us),
         "cpu_baseline": cpu,
         "configs": configs,
         "sweep": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}

@@ -1142,6 +1142,57 @@ extern "C" hipError_t qe_attn_prep_decode(const void* qg, const void* k, const v
                                 stream);
 }
 
-extern "C" const char* qe_attn_version(void) { return "qengine_amd attn 0.1 (gfx950)"; }
+// ---------------------------------------------------------------------------- measurement only
+namespace qe {
+// The K and V bytes one decode call reads, with the partials kernel's grid and slices, and no
+// arithmetic: workgroup (s, g) streams rows [s*CH, min((s+1)*CH, L)) of K and V of KV head g, 256
+// threads, 8 + 8 sixteen-byte non-temporal loads in flight per thread. Its time bounds any kernel
+// that must read those bytes with that grid.
+__global__ void __launch_bounds__(256)
+kv_stream_probe_kernel(const __bf16* __restrict__ kc, const __bf16* __restrict__ vc, int L,
+                       int max_len, int CH, uint32_t* __restrict__ sink) {
+  const int s = blockIdx.x, g = blockIdx.y;
+  const int beg = s * CH, end = min(beg + CH, L);
+  if (beg >= end) return;
+  const size_t head = (size_t)g * max_len * HD;
+  const uint32_t bytes = (uint32_t)end * (HD * 2);
+  const __amdgpu_buffer_rsrc_t kr = make_rsrc_uniform(kc + head, bytes);
+  const __amdgpu_buffer_rsrc_t vr = make_rsrc_uniform(vc + head, bytes);
+  uint32_t acc = 0;
+  for (uint32_t off = (uint32_t)beg * (HD * 2) + threadIdx.x * 16; off < bytes;
+       off += 256 * 16 * 8) {
+    u32x4_t a[8], b[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      a[j] = buffer_load16_stream(kr, off + j * 4096);  // past the slice end: 0, no traffic
+      b[j] = buffer_load16_stream(vr, off + j * 4096);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc ^= a[j][0] ^ a[j][1] ^ a[j][2] ^ a[j][3] ^ b[j][0] ^ b[j][1] ^ b[j][2] ^ b[j][3];
+  }
+  if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+__global__ void __launch_bounds__(WAVE) launch_probe_kernel() {}
+}  // namespace qe
+
+extern "C" hipError_t qe_kv_stream_probe(const void* kc, const void* vc, int L, int Hkv,
+                                         int max_len, int NS, void* sink, hipStream_t stream) {
+  if (L < 1 || L > max_len || Hkv < 1 || NS < 1 || !kc || !vc || !sink ||
+      (unsigned long long)max_len * HD * 2 >= (1ull << 32) || max_len >= SPLIT_L_MAX)
+    return hipErrorInvalidValue;
+  const int CH = split_size(L, ns_div(NS));
+  kv_stream_probe_kernel<<<dim3((L + CH - 1) / CH, Hkv), dim3(256), 0, stream>>>(
+      static_cast<const __bf16*>(kc), static_cast<const __bf16*>(vc), L, max_len, CH,
+      static_cast<uint32_t*>(sink));
+  return hipGetLastError();
+}
+
+extern "C" hipError_t qe_launch_probe(hipStream_t stream) {
+  launch_probe_kernel<<<dim3(1), dim3(WAVE), 0, stream>>>();
+  return hipGetLastError();
+}
+
+extern "C" const char* qe_attn_version(void) { return "qengine_amd attn 0.2 (gfx950)"; }
 extern "C" void qe_set_pdl_trigger(int) {}
 extern "C" void qe_set_pdl_launch(int) {}
