@@ -211,7 +211,7 @@ def bench_length(torch, C, qa, L: int, steps: int, warmup: int, ns: int | None):
 
     def probe_all(s):
         for k, v in zip(s.kc, s.vc):
-            capi.kv_stream_probe(k, v, L, HKV, L, ns, sink)
+            capi.kv_stream_probe(k, v, s.pos, HKV, L, ns, sink)
     full = [capture(torch, s.decode_all) for s in sets]
     part = [capture(torch, s.partials_all) for s in sets]
     probe = [capture(torch, lambda s=s: probe_all(s)) for s in sets]

@@ -138,13 +138,14 @@ hipError_t qe_attn_decode_fp8_partials(const void* q, const void* kc8, const voi
                                        float k_scale, hipStream_t stream);
 
 /* Measurement only (no counterpart in the reference). A streaming read of exactly the K and V
- * bytes a 1-row decode call attending L positions reads, with the partials kernel's grid
- * (slices of qe_attn_split_size(L, NS) positions x Hkv heads, 256 threads per workgroup,
- * 16-byte non-temporal loads) and no arithmetic: the floor of any kernel that reads those bytes
- * with that grid. `sink` (4 bytes of device memory) is written only if the folded value hits a
- * constant. Valid: 1 <= L <= max_len, Hkv >= 1, NS >= 1, max_len*512 < 2^32. */
-hipError_t qe_kv_stream_probe(const void* kc, const void* vc, int L, int Hkv, int max_len, int NS,
-                              void* sink, hipStream_t stream);
+ * bytes a 1-row decode call at position *pos reads (L = min(*pos+1, max_len) positions), with
+ * the partials kernel's grid and slicing (slices of qe_attn_split_size(L, NS) positions x Hkv
+ * heads, pos read on the device, 256 threads per workgroup, 16-byte non-temporal loads) and no
+ * arithmetic: the floor of any kernel that reads those bytes with that grid. `sink` (4 bytes of
+ * device memory) is written only if the folded value hits a constant.
+ * Valid: max_len >= 1, Hkv >= 1, NS >= 1, max_len*512 < 2^32. */
+hipError_t qe_kv_stream_probe(const void* kc, const void* vc, const int* pos, int Hkv,
+                              int max_len, int NS, void* sink, hipStream_t stream);
 
 /* Measurement only: one empty one-wave kernel. Its time per node in a hipGraph of such launches
  * is the per-launch floor every graph node pays. */

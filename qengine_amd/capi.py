@@ -30,7 +30,7 @@ SIGNATURES = {
     "qe_attn_prep_decode": (_I, [_P, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _I, _I,
                                  _I, _I, _I, _I, _F, _F, _P]),
     "qe_attn_split_size": (_I, [_I, _I]),
-    "qe_kv_stream_probe": (_I, [_P, _P, _I, _I, _I, _I, _P, _P]),
+    "qe_kv_stream_probe": (_I, [_P, _P, _P, _I, _I, _I, _P, _P]),
     "qe_launch_probe": (_I, [_P]),
     "qe_attn_version": (ctypes.c_char_p, []),
     "qe_set_pdl_trigger": (None, [_I]),
@@ -142,10 +142,10 @@ def split_size(L: int, ns: int) -> int:
     return load().qe_attn_split_size(L, ns)
 
 
-def kv_stream_probe(kc, vc, L, hkv, max_len, ns, sink, stream=None) -> int:
-    """Measurement only: stream the K/V bytes of a 1-row decode at L positions with the partials
-    kernel's grid, no arithmetic (qe_kv_stream_probe)."""
-    return load().qe_kv_stream_probe(_ptr(kc), _ptr(vc), L, hkv, max_len, ns, _ptr(sink),
+def kv_stream_probe(kc, vc, pos, hkv, max_len, ns, sink, stream=None) -> int:
+    """Measurement only: stream the K/V bytes of a 1-row decode at device position pos with the
+    partials kernel's grid and slicing, no arithmetic (qe_kv_stream_probe)."""
+    return load().qe_kv_stream_probe(_ptr(kc), _ptr(vc), _ptr(pos), hkv, max_len, ns, _ptr(sink),
                                      _stream(stream))
 
 

@@ -554,6 +554,59 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
 #pragma unroll
     for (int ct = 0; ct < NT; ++ct) l[ct] = group4_sum(l[ct]);
 
+    static_assert(WAVES == 4, "merge layout assumes 4 waves");
+    f32x4_t (*s_acc)[16][WAVE] = reinterpret_cast<f32x4_t (*)[16][WAVE]>(lds);
+    if constexpr (NT == 1) {
+      // One barrier: each wave parks (m, l) and the accumulators of the pass's columns in its own
+      // K tile's LDS (s_acc[w] is exactly that region, which no other wave touches), then thread
+      // (w, lane) merges h = w/2, i in [4(w&1), +4) over waves 0..3 in that order and writes
+      // 4 x 16 bytes: dims 128h + 32g4 + 8ii + 4(w&1) + [0, 4) for ii = 0..3. Same arithmetic
+      // and order as the NT >= 2 merge below, so the bits do not depend on NT.
+      const int col = c;
+      const bool mine = in_pass(col, grp, P);
+      if (g4 == 0) {
+        s_m[w][col] = m[0];
+        s_l[w][col] = l[0];
+      }
+      if (mine) {
+#pragma unroll
+        for (int a = 0; a < 16; ++a) s_acc[w][a][lane] = acc[0][a];
+      }
+      __syncthreads();
+      if (!mine) return;
+      float M = -INFINITY, wsc[WAVES];
+#pragma unroll
+      for (int v = 0; v < WAVES; ++v) M = fmaxf(M, s_m[v][col]);
+      float L = 0.f;
+#pragma unroll
+      for (int v = 0; v < WAVES; ++v) {
+        const float mv = s_m[v][col];
+        wsc[v] = mv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv - M);
+        L += s_l[v][col] * wsc[v];
+      }
+      const int t = trow[0], head = g * grp + (col - t * grp);
+      if (w == 0 && g4 == 0) {
+        float* ml = part_ml + (((size_t)t * Hq + head) * NS + s) * 2;
+        ml[0] = M;
+        ml[1] = L;
+      }
+      const int h = w >> 1, i0 = 4 * (w & 1);
+      f32x4_t mo[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        f32x4_t sum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int v = 0; v < WAVES; ++v) sum += s_acc[v][8 * h + i0 + k][lane] * wsc[v];
+        mo[k] = sum;
+      }
+      float* dst = part_o + (((size_t)t * Hq + head) * NS + s) * HD + 128 * h + 32 * g4 + i0;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii)
+        reinterpret_cast<f32x4_t*>(dst + 8 * ii)[0] =
+            f32x4_t{mo[0][ii], mo[1][ii], mo[2][ii], mo[3][ii]};
+      return;
+    }
+
     if (g4 == 0) {
 #pragma unroll
       for (int ct = 0; ct < NT; ++ct) {
@@ -589,9 +642,7 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
     // other columns stay idle, which keeps the LDS traffic to what the merge needs), one barrier,
     // then thread (w, lane) merges h = w/2, i in [4(w&1), +4) over waves 0..3 in that order and
     // writes 4 x 16 bytes: dims 128h + 32g4 + 8ii + 4(w&1) + [0, 4) for ii = 0..3.
-    static_assert(WAVES == 4, "merge layout assumes 4 waves");
     static_assert(WAVES * 16 * WAVE * 16 <= lds_k_bytes<WAVES>(), "merge buffer aliases the K tiles");
-    f32x4_t (*s_acc)[16][WAVE] = reinterpret_cast<f32x4_t (*)[16][WAVE]>(lds);
 #pragma unroll
     for (int ct = 0; ct < NT; ++ct) {
       const int col = ct * 16 + c;
@@ -1144,13 +1195,17 @@ extern "C" hipError_t qe_attn_prep_decode(const void* qg, const void* k, const v
 
 // ---------------------------------------------------------------------------- measurement only
 namespace qe {
-// The K and V bytes one decode call reads, with the partials kernel's grid and slices, and no
-// arithmetic: workgroup (s, g) streams rows [s*CH, min((s+1)*CH, L)) of K and V of KV head g, 256
-// threads, 8 + 8 sixteen-byte non-temporal loads in flight per thread. Its time bounds any kernel
-// that must read those bytes with that grid.
+// The K and V bytes a 1-row decode call reads, with the partials kernel's grid, its slicing (from
+// the device scalar pos, as the decode does) and no arithmetic: workgroup (s, g) streams rows
+// [s*CH, min((s+1)*CH, L)) of K and V of KV head g, 256 threads, 8 + 8 sixteen-byte
+// non-temporal loads in flight per thread. Its time bounds any kernel that must read those bytes
+// with that grid.
 __global__ void __launch_bounds__(256)
-kv_stream_probe_kernel(const __bf16* __restrict__ kc, const __bf16* __restrict__ vc, int L,
-                       int max_len, int CH, uint32_t* __restrict__ sink) {
+kv_stream_probe_kernel(const __bf16* __restrict__ kc, const __bf16* __restrict__ vc,
+                       const int* __restrict__ pos_ptr, int max_len, NsDiv nd,
+                       uint32_t* __restrict__ sink) {
+  const int L = min(pos_ptr[0] + 1, max_len);
+  const int CH = split_size(L, nd);
   const int s = blockIdx.x, g = blockIdx.y;
   const int beg = s * CH, end = min(beg + CH, L);
   if (beg >= end) return;
@@ -1168,7 +1223,8 @@ kv_stream_probe_kernel(const __bf16* __restrict__ kc, const __bf16* __restrict__
       b[j] = buffer_load16_stream(vr, off + j * 4096);
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc ^= a[j][0] ^ a[j][1] ^ a[j][2] ^ a[j][3] ^ b[j][0] ^ b[j][1] ^ b[j][2] ^ b[j][3];
+    for (int j = 0; j < 8; ++j)
+      acc ^= a[j][0] ^ a[j][1] ^ a[j][2] ^ a[j][3] ^ b[j][0] ^ b[j][1] ^ b[j][2] ^ b[j][3];
   }
   if (acc == 0x9E3779B9u) sink[0] = acc;
 }
@@ -1176,14 +1232,13 @@ kv_stream_probe_kernel(const __bf16* __restrict__ kc, const __bf16* __restrict__
 __global__ void __launch_bounds__(WAVE) launch_probe_kernel() {}
 }  // namespace qe
 
-extern "C" hipError_t qe_kv_stream_probe(const void* kc, const void* vc, int L, int Hkv,
+extern "C" hipError_t qe_kv_stream_probe(const void* kc, const void* vc, const int* pos, int Hkv,
                                          int max_len, int NS, void* sink, hipStream_t stream) {
-  if (L < 1 || L > max_len || Hkv < 1 || NS < 1 || !kc || !vc || !sink ||
-      (unsigned long long)max_len * HD * 2 >= (1ull << 32) || max_len >= SPLIT_L_MAX)
+  if (max_len < 1 || Hkv < 1 || NS < 1 || !kc || !vc || !pos || !sink ||
+      (unsigned long long)max_len * HD * 2 >= (1ull << 32))
     return hipErrorInvalidValue;
-  const int CH = split_size(L, ns_div(NS));
-  kv_stream_probe_kernel<<<dim3((L + CH - 1) / CH, Hkv), dim3(256), 0, stream>>>(
-      static_cast<const __bf16*>(kc), static_cast<const __bf16*>(vc), L, max_len, CH,
+  kv_stream_probe_kernel<<<dim3(max_slices(max_len, NS), Hkv), dim3(256), 0, stream>>>(
+      static_cast<const __bf16*>(kc), static_cast<const __bf16*>(vc), pos, max_len, ns_div(NS),
       static_cast<uint32_t*>(sink));
   return hipGetLastError();
 }

@@ -428,3 +428,20 @@ def test_layer_multi_row_passes_match_token_by_token(native):
     ok, err = ulp_close(layer.kc.cpu(), kc_ref, ulps=1)
     assert ok, err
     assert torch.equal(layer.vc.cpu(), vc_ref)
+
+
+def test_measurement_probes_run(capi):
+    """The ceiling probes of the bench (measurement only) launch and return hipSuccess; the
+    stream probe's sink stays untouched (the folded value never hits the sentinel on N(0,1)
+    data), and an empty launch returns hipSuccess too."""
+    L, hkv = 4096, 4
+    g = torch.Generator(device=DEV).manual_seed(3)
+    kc = torch.randn(hkv, L, D, device=DEV, generator=g).to(BF)
+    vc = torch.randn(hkv, L, D, device=DEV, generator=g).to(BF)
+    sink = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for p in (0, 100, L - 1, L + 50):
+        pos = torch.tensor([p], dtype=torch.int32, device=DEV)
+        assert capi.kv_stream_probe(kc, vc, pos, hkv, L, 64, sink) == 0
+    assert capi.launch_probe() == 0
+    torch.cuda.synchronize()
+    assert int(sink.item()) == 0
