@@ -75,6 +75,21 @@ hipError_t qe_attn_decode_partials(const void* q, const void* kc, const void* vc
                                    float* part_o, float* part_ml, int n, int Hq, int Hkv,
                                    int max_len, int NS, float scale, hipStream_t stream);
 
+/* qe_attn_decode without caller scratch: the same kernels and the same bits, with part_o /
+ * part_ml in a file-scope device array of the library (QE_NOALLOC_MAX_SLOTS (row, head, slice)
+ * triples: 12,288 x 258 fp32 = 12.7 MB, held on every GPU the library runs on until the process
+ * ends). The call allocates nothing (no hipMalloc, hipFree or allocating library routine); on its
+ * first call on a device it looks the array's address up once (hipGetSymbolAddress, with that
+ * device current). Valid as qe_attn_decode, plus n*Hq*NS <= QE_NOALLOC_MAX_SLOTS
+ * (hipErrorInvalidValue otherwise). Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, other host threads) race. Nothing in the array needs to
+ * start at zero. No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under hipGraph capture, tight serving loops, harnesses that forbid hipMalloc). */
+#define QE_NOALLOC_MAX_SLOTS 12288
+hipError_t qe_attn_decode_noalloc(const void* q, const void* kc, const void* vc, const int* pos,
+                                  const void* qg, long ldp, void* out, long ldo, int n, int Hq,
+                                  int Hkv, int max_len, int NS, float scale, hipStream_t stream);
+
 /* Second half of qe_attn_decode: log-sum-exp combine of the partials + sigmoid output gate.
  * No counterpart in the reference (see qe_attn_decode_partials). */
 hipError_t qe_attn_decode_combine(const float* part_o, const float* part_ml, const int* pos,

@@ -24,6 +24,7 @@ SIGNATURES = {
     "qe_attn_prep": (_I, [_P, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P]),
     "qe_attn_decode": (_I, [_P, _P, _P, _P, _P, _L, _P, _P, _P, _L, _I, _I, _I, _I, _I, _F, _P]),
     "qe_attn_decode_partials": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P]),
+    "qe_attn_decode_noalloc": (_I, [_P, _P, _P, _P, _P, _L, _P, _L, _I, _I, _I, _I, _I, _F, _P]),
     "qe_attn_decode_combine": (_I, [_P, _P, _P, _P, _L, _P, _L, _I, _I, _I, _I, _P]),
     "qe_attn_prefill": (_I, [_P, _P, _P, _P, _P, _L, _P, _L, _I, _I, _I, _I, _F, _P]),
     "qe_attn_prefill_fp8": (_I, [_P, _P, _P, _P, _P, _L, _P, _L, _I, _I, _I, _I, _F, _F, _F, _P]),
@@ -101,6 +102,17 @@ def decode(q, kc, vc, pos, qg, ldp, part_o, part_ml, out, ldo, n, hq, hkv, max_l
     return load().qe_attn_decode(_ptr(q), _ptr(kc), _ptr(vc), _ptr(pos), _ptr(qg), ldp,
                                  _ptr(part_o), _ptr(part_ml), _ptr(out), ldo, n, hq, hkv, max_len,
                                  ns, scale, _stream(stream))
+
+
+NOALLOC_MAX_SLOTS = 12288  # QE_NOALLOC_MAX_SLOTS in include/qe_attn.h
+
+
+def decode_noalloc(q, kc, vc, pos, qg, ldp, out, ldo, n, hq, hkv, max_len, ns, scale=1.0 / 16,
+                   stream=None) -> int:
+    """qe_attn_decode with the library's own device scratch (no caller part_o / part_ml)."""
+    return load().qe_attn_decode_noalloc(_ptr(q), _ptr(kc), _ptr(vc), _ptr(pos), _ptr(qg), ldp,
+                                         _ptr(out), ldo, n, hq, hkv, max_len, ns, scale,
+                                         _stream(stream))
 
 
 def prep_decode(qg, k, v, ldp, qnw, knw, inv_freq, pos, q_out, kc, vc, part_o, part_ml, out, ldo,

@@ -27,6 +27,7 @@
 //    moved (an exact no-op).
 //  * Buffer resources bound the K/V reads to the slice: positions past it load as 0.
 //  * A second launch merges the slices (log-sum-exp) and applies the sigmoid gate.
+#include <mutex>
 #include <utility>
 
 #include "attn_tile.hpp"
@@ -1105,6 +1106,54 @@ extern "C" hipError_t qe_attn_decode(const void* q, const void* kc, const void* 
   if (e != hipSuccess) return e;
   return qe_attn_decode_combine(part_o, part_ml, pos, qg, ldp, out, ldo, n, Hq, max_len, NS,
                                 stream);
+}
+
+// ---------------------------------------------------------------- decode without caller scratch
+// The split-KV partials of qe_attn_decode_noalloc live in this file-scope device array: part_o
+// [n][Hq][NS][256] then part_ml [n][Hq][NS][2] (fp32), for at most QE_NOALLOC_MAX_SLOTS (row,
+// head, slice) triples. Every GPU the library runs on holds its own copy until the process ends.
+// In host code `scratch` names a host-side stand-in, never the device memory: its per-device
+// address comes from hipGetSymbolAddress and is used everywhere instead.
+static __device__ __align__(256) float scratch[QE_NOALLOC_MAX_SLOTS * (HD + 2)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up once per device (with that device
+// current) and kept.
+hipError_t scratch_of_current_device(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+}  // namespace
+
+extern "C" hipError_t qe_attn_decode_noalloc(const void* q, const void* kc, const void* vc,
+                                             const int* pos, const void* qg, long ldp, void* out,
+                                             long ldo, int n, int Hq, int Hkv, int max_len, int NS,
+                                             float scale, hipStream_t stream) {
+  hipError_t e = check_decode_shape(n, Hq, Hkv, max_len, NS);
+  if (e != hipSuccess) return e;
+  if ((long long)n * Hq * NS > QE_NOALLOC_MAX_SLOTS) return hipErrorInvalidValue;
+  float* base = nullptr;
+  e = scratch_of_current_device(&base);
+  if (e != hipSuccess) return e;
+  float* part_o = base;
+  float* part_ml = base + (size_t)QE_NOALLOC_MAX_SLOTS * HD;
+  return qe_attn_decode(q, kc, vc, pos, qg, ldp, part_o, part_ml, out, ldo, n, Hq, Hkv, max_len,
+                        NS, scale, stream);
 }
 
 static bool kv_scales_ok(float k_scale, float v_scale) {
