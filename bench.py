@@ -566,7 +566,7 @@ def bench_gdn(torch, C, steps: int, warmup: int) -> dict:
                      *Ld["st"], ctl, out[:n], hk, 1e-6)
 
     res = {}
-    for n in (1, 4, 8):
+    for n in (1, 2, 4, 6, 8):
         sets = [[layer() for _ in range(nl)] for _ in range(2)]
         prime = torch.tensor([100, 0, 0, 0, 0, 0, 0, 0], dtype=I32, device=dev)
         ctl = torch.tensor([100, n, 0, 0, 0, 0, 0, 0], dtype=I32, device=dev)

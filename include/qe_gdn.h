@@ -32,9 +32,10 @@ extern "C" {
  * writes S), runs its n rows on a copy, stages them, and writes the ring slots pos .. pos+n-1.
  * The caller then sets pos += kept, pending = kept.
  * Valid: 1 <= n <= 8, Hk >= 1, Hv % Hk == 0, Hv <= 65535, C < 2^26, ldp >= C, ldo >= Hv*128.
- * Two calls must not run concurrently on one device: with 2-8 rows and Hv <= 64 the kernel
- * splits each head over 4 workgroups that exchange partial sums through a 16 KB table the library
- * holds per device (calls on one stream, as in a decode step, are always fine).
+ * A call touches no memory but its arguments, so calls on different layers (different state,
+ * ring, staging and output buffers) may run concurrently on any streams; calls that share those
+ * buffers must be ordered, as in the reference. 5-8 rows run as two launches (each head split over
+ * 4 workgroups, then a per-head finish); no workgroup waits for another.
  * Replaces launch_gdn_step_n (reference csrc/ops.h:20-23, csrc/gdn.cu:65-341). The reference's
  * thread-split argument `q` selects a CUDA block shape; it has no counterpart here. */
 hipError_t qe_gdn_step_n(const void* qkv, const void* z, const void* b, const void* a, long ldp,

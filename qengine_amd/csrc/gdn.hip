@@ -12,9 +12,9 @@
 // The same inline update runs for replayed and new rows, so the committed state after any
 // pattern of calls with kept prefixes equals plain one-row decoding bit for bit.
 //
-// Two kernels share the per-column arithmetic and so give the same bits: gdn_step_kernel (one
-// workgroup per head, below) for 1-row calls and large Hv, and gdn_split_kernel (each head over
-// 4 workgroups, further down) for 2-8 rows when its grid fits the GPU at once.
+// Two paths share the per-column arithmetic and so give the same bits: gdn_step_kernel (one
+// workgroup per head, below) for 1-4 rows, and gdn_split_kernel (each head over 4 workgroups)
+// followed by gdn_finish_kernel (further down) for 5-8 rows.
 //
 // gfx950 layout: one 512-thread workgroup (8 waves) per value head. Wave w owns state columns
 // 16w .. 16w+15; lane l holds rows 8(l>>2) .. +7 of columns 16w + 4(l&3) .. +3 (32 fp32 registers,
@@ -47,8 +47,7 @@ constexpr int GDN_THREADS = 512;
 constexpr int GDN_SPLIT = 4;                        // workgroups per head in the split kernel
 constexpr int GDN_SPLIT_COLS = GDN_D / GDN_SPLIT;
 constexpr int GDN_SPLIT_THREADS = 512;
-constexpr int GDN_SPLIT_MAX_HV = 64;                // exchange table size (heads)
-constexpr int GDN_SPIN_LIMIT = 1 << 18;
+constexpr int GDN_SPLIT_MIN_ROWS = 5;               // fewer rows: the one-workgroup kernel
 
 struct __align__(16) F4 {
   float x, y, z, w;
@@ -131,6 +130,32 @@ __device__ __forceinline__ void lds_read8(const float* p, float (&d)[8]) {
 __device__ __forceinline__ void lds_read4(const float* p, float (&d)[4]) {
   const F4 a = *reinterpret_cast<const F4*>(p);
   d[0] = a.x; d[1] = a.y; d[2] = a.z; d[3] = a.w;
+}
+
+// Gated RMSNorm of one output row of a head (wave-wide; lane holds columns 2 lane, 2 lane + 1):
+// out = bf16(bf16(w * bf16(o * r)) * silu(z)), r = 1 / sqrt(sum(o^2) / 128 + eps). The sum of
+// squares is four serial 32-column partials added in order, the same in every kernel, so every
+// path gives the same bits.
+__device__ __forceinline__ void gated_norm_row(const float* __restrict__ o_row, int lane, float nw0,
+                                               float nw1, float z0, float z1, float eps,
+                                               __bf16* __restrict__ op) {
+  const float2 o = *reinterpret_cast<const float2*>(&o_row[2 * lane]);
+  float part_ss = 0.f;
+  if (lane < GDN_SPLIT) {
+#pragma unroll
+    for (int cc = 0; cc < GDN_D / GDN_SPLIT; ++cc)
+      part_ss = fmaf(o_row[lane * (GDN_D / GDN_SPLIT) + cc], o_row[lane * (GDN_D / GDN_SPLIT) + cc],
+                     part_ss);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int g = 0; g < GDN_SPLIT; ++g)
+    ss += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part_ss), g));
+  const float inv = 1.0f / sqrtf(ss / 128.0f + eps);
+  const float y0 = round_bf16(nw0 * round_bf16(o.x * inv));  // bf16 weight * bf16 norm
+  const float y1 = round_bf16(nw1 * round_bf16(o.y * inv));
+  op[2 * lane] = f32_to_bf16(y0 * silu_f(z0));
+  op[2 * lane + 1] = f32_to_bf16(y1 * silu_f(z1));
 }
 
 __global__ void __launch_bounds__(GDN_THREADS)
@@ -282,75 +307,44 @@ gdn_step_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
   __syncthreads();
 
   // ---- gated RMSNorm: wave t normalises row t ----
-  if (w < n) {
-    const float2 o = *reinterpret_cast<const float2*>(&oa[w][2 * lane]);
-    // Sum of squares in the split kernel's order (four serial 32-column partials, added in
-    // order), so both kernels give the same bits and a call may use either.
-    float part_ss = 0.f;
-    if (lane < GDN_SPLIT) {
-#pragma unroll
-      for (int cc = 0; cc < GDN_D / GDN_SPLIT; ++cc)
-        part_ss = fmaf(oa[w][lane * (GDN_D / GDN_SPLIT) + cc], oa[w][lane * (GDN_D / GDN_SPLIT) + cc],
-                       part_ss);
-    }
-    float ss = 0.f;
-#pragma unroll
-    for (int g = 0; g < GDN_SPLIT; ++g)
-      ss += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part_ss), g));
-    const float inv = 1.0f / sqrtf(ss / 128.0f + eps);
-    const float y0 = round_bf16(nw0 * round_bf16(o.x * inv));  // bf16 weight * bf16 norm
-    const float y1 = round_bf16(nw1 * round_bf16(o.y * inv));
-    __bf16* op = out + (size_t)w * ldo + j * GDN_D + 2 * lane;
-    op[0] = f32_to_bf16(y0 * silu_f(z0));
-    op[1] = f32_to_bf16(y1 * silu_f(z1));
-  }
+  if (w < n) gated_norm_row(oa[w], lane, nw0, nw1, z0, z1, eps, out + (size_t)w * ldo + j * GDN_D);
 }
 
-// ------------------------------------------------------------------ split kernel
-// The same step with each head's 128 state columns split over GDN_SPLIT workgroups of 256
+// ------------------------------------------------------------------ split kernels
+// The same step with each head's 128 state columns split over GDN_SPLIT workgroups of 512
 // threads (32 columns each): four times the CUs for the state I/O and the delta-rule VALU work,
-// which bound the one-workgroup kernel. Each workgroup holds rows 8 rg .. +7 of two columns per
-// lane (wave w: local columns 8w .. 8w+7) and runs the same per-column arithmetic, so the state
-// is bit-identical to the one-workgroup kernel's. Every workgroup repeats the conv, l2norm and
-// gates of its head's q and k (256 channels) and does the v channels of its own columns.
+// which bound the one-workgroup kernel. Each workgroup holds rows 8 rg .. +7 of its columns per
+// lane and runs the same per-column arithmetic, so the state is bit-identical to the
+// one-workgroup kernel's. Every workgroup repeats the conv, l2norm and gates of its head's q and
+// k (256 channels) and does the v channels of its own columns.
 //
-// The gated RMSNorm needs the sum of squares of the head's 128 outputs of a row, spread over
-// the G workgroups. Each publishes its partial sum through a 64-bit {tag, value} slot per
-// (head, row, workgroup) in gdn_xchg, written and polled with relaxed device-scope atomics (one
-// location carries both the tag and the value, so no fence is needed), and sums the G partials
-// in slot order, so all G workgroups apply the same factor. Tags: every call with n > t adds 1
-// to all G slots of (head, row t), so the G slots of a row always hold equal tags between calls
-// and a workgroup expects its own slot's tag + 1 from the others. The wait needs every
-// workgroup of the grid resident at once: the host launches this kernel only when 4 Hv is at
-// most the device's CU count (one workgroup per CU always fits; 8 waves, < 80 VGPRs, 16 KB LDS),
-// and falls back to the one-workgroup kernel otherwise. The polling is bounded all the same:
-// past GDN_SPIN_LIMIT polls the row's outputs are NaN instead of a hang. Block b runs head
-// b % Hv, part b / Hv: with Hv a multiple of 8 the parts of a head share an XCD.
-//
-// The slots are one table per device, so two calls must not run concurrently on one device
-// (calls on one stream, as in a decode step, are fine).
-
-__device__ unsigned long long gdn_xchg[GDN_SPLIT_MAX_HV][GDN_MAXN][GDN_SPLIT];
+// Nothing waits across workgroups. What needs a whole head (the gated RMSNorm sums the squares
+// of a row's 128 outputs) or must not overwrite what another part still reads (the staged k rows
+// and gates of the previous call, which every part of a head replays) is left to a second
+// kernel, gdn_finish_kernel: gdn_split_kernel writes each row's outputs o, already bf16 values,
+// into `out` unnormalised, and stages only its own v columns; gdn_finish_kernel (one workgroup
+// per head, after every part has finished) recomputes the head's normalised k rows and gates with
+// the same arithmetic, stages them, and normalises `out` in place. Block b runs head b % Hv, part
+// b / Hv: with Hv a multiple of 8 the parts of a head share an XCD.
 
 // NT = 256: four waves, two columns per lane; NT = 512: eight waves (two per SIMD, so one wave's
 // reduction and LDS latencies hide behind the other's), one column per lane, and the v channels
 // and gates on threads of their own (256 .. 287, 288 ..) instead of a second role.
 template <int NT>
 __global__ void __launch_bounds__(NT)
-gdn_split_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
-                 const __bf16* __restrict__ b, const __bf16* __restrict__ a, long ldp,
-                 __bf16* __restrict__ ring, const __bf16* __restrict__ conv_w,
-                 const __bf16* __restrict__ A_log, const __bf16* __restrict__ dt_bias,
-                 const __bf16* __restrict__ norm_w, float* __restrict__ S,
+gdn_split_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ b,
+                 const __bf16* __restrict__ a, long ldp, __bf16* __restrict__ ring,
+                 const __bf16* __restrict__ conv_w, const __bf16* __restrict__ A_log,
+                 const __bf16* __restrict__ dt_bias, float* __restrict__ S,
                  float* __restrict__ st_k, float* __restrict__ st_v, float* __restrict__ st_g,
                  const int* __restrict__ ctl, __bf16* __restrict__ out, long ldo, int n, int Hk,
-                 int Hv, float eps) {
+                 int Hv) {
   constexpr int CW = GDN_SPLIT_COLS;
   constexpr int NC = 512 / NT;  // state columns per lane
   __shared__ __align__(16) float sk[GDN_MAXN][GDN_D], sv[GDN_MAXN][CW];  // replayed rows
   __shared__ __align__(16) float qa[GDN_MAXN][GDN_D], ka[GDN_MAXN][GDN_D], va[GDN_MAXN][CW];
   __shared__ __align__(16) float oa[GDN_MAXN][CW];
-  __shared__ float sg[GDN_MAXN][2], ga[GDN_MAXN][2], l2p[GDN_MAXN][4], sst[GDN_MAXN];
+  __shared__ float sg[GDN_MAXN][2], ga[GDN_MAXN][2], l2p[GDN_MAXN][4];
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int j = blockIdx.x % Hv, g = blockIdx.x / Hv;
@@ -363,9 +357,6 @@ gdn_split_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
   // Loads, all unconditional with in-bounds indices (as in the one-workgroup kernel).
   const int P = ctl[0];
   const int pend = min(max(ctl[1], 0), GDN_MAXN);
-  // own exchange tag of row tid & 7 (threads 0 .. n-1 use theirs)
-  const unsigned long long tagword =
-      __hip_atomic_load(&gdn_xchg[j][tid & 7][g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const bool qk_thread = tid < 2 * GDN_D;             // q (part 0) or k (part 1) channel c
   const int part = (tid >> 7) & 1, c = tid & 127;
   const int ch = (part * Hk + i) * GDN_D + c;
@@ -386,8 +377,6 @@ gdn_split_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
   const __bf16 bb = b[(size_t)gtc * ldp + j], ab = a[(size_t)gtc * ldp + j];
   const __bf16 dtb = dt_bias[j], alb = A_log[j];
   const int ot = (tid >> 5) & 7, oc = tid & (CW - 1);  // output element (row ot, column cb + oc)
-  const __bf16 zb = z[(size_t)min(ot, n - 1) * ldp + j * GDN_D + cb + oc];
-  const __bf16 nwb = norm_w[cb + oc];
   __bf16 hb[3], hbv[3];
 #pragma unroll
   for (int q = 0; q < 3; ++q) {
@@ -461,8 +450,8 @@ gdn_split_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
 
   // Stage this call's v columns for the next call (after the barrier: this workgroup's reads of
   // the previous call's rows at the same addresses are in LDS by now; no other workgroup reads
-  // these columns). The k rows and gates, which every part of the head reads, are staged after
-  // the exchange below.
+  // these columns). The k rows and gates, which every part of the head reads, are staged by
+  // gdn_finish_kernel.
   if (qk_thread && ot < n) st_v[((size_t)ot * Hv + j) * GDN_D + cb + oc] = va[ot][oc];
   if (qk_thread) {
     const float sqrt_dk = 11.313708498984761f;  // sqrt(128) rounded to fp32
@@ -511,67 +500,105 @@ gdn_split_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
   }
   __syncthreads();
 
-  // ---- 3. sum of squares of the head's 128 outputs of each row, across the G workgroups ----
-  if (tid < n) {
-    const int t = tid;
-    float part_ss = 0.f;
+  // ---- 3. this workgroup's columns of each row's output, unnormalised (o is a bf16 value, so
+  // `out` holds it exactly); gdn_finish_kernel normalises the whole row ----
+  if (qk_thread && ot < n) out[(size_t)ot * ldo + j * GDN_D + cb + oc] = f32_to_bf16(oa[ot][oc]);
+}
+
+// Second kernel of a split call, one 256-thread workgroup per value head j, after every part of
+// gdn_split_kernel has finished (so no part still reads the previous call's staged rows):
+//   * threads 0-127 recompute the normalised k channel c of this call's rows (conv + SiLU from
+//     the ring history and the input rows, the sum of squares of waves 0 and 1 added in that
+//     order, as gdn_split_kernel's waves 2 and 3 add it) and stage it; threads 128 .. 128+n-1
+//     stage the gates;
+//   * wave w normalises rows w and w + 4 of the head's outputs in place (gated_norm_row).
+__global__ void __launch_bounds__(256)
+gdn_finish_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
+                  const __bf16* __restrict__ b, const __bf16* __restrict__ a, long ldp,
+                  const __bf16* __restrict__ ring, const __bf16* __restrict__ conv_w,
+                  const __bf16* __restrict__ A_log, const __bf16* __restrict__ dt_bias,
+                  const __bf16* __restrict__ norm_w, float* __restrict__ st_k,
+                  float* __restrict__ st_g, const int* __restrict__ ctl, __bf16* __restrict__ out,
+                  long ldo, int n, int Hk, int Hv, float eps) {
+  __shared__ __align__(16) float oa[GDN_MAXN][GDN_D];
+  __shared__ float l2p[GDN_MAXN][2];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int j = blockIdx.x, i = j / (Hv / Hk);
+  const int C = 2 * Hk * GDN_D + Hv * GDN_D;
+  const int P = ctl[0];
+  const int c = tid & 127;
+  const int ch = (Hk + i) * GDN_D + c;  // k channel c of qk head i
+  const uint2 wk = *reinterpret_cast<const uint2*>(conv_w + (size_t)ch * 4);
+  __bf16 xb[GDN_MAXN], hb[3];
 #pragma unroll
-    for (int cc = 0; cc < CW; ++cc) part_ss = fmaf(oa[t][cc], oa[t][cc], part_ss);
-    const unsigned tag = (unsigned)(tagword >> 32) + 1u;
-    __hip_atomic_store(&gdn_xchg[j][t][g],
-                       ((unsigned long long)tag << 32) | __float_as_uint(part_ss),
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    unsigned long long v[GDN_SPLIT];
-    bool done = false;
-    for (int it = 0; it < GDN_SPIN_LIMIT && !done; ++it) {
+  for (int t = 0; t < GDN_MAXN; ++t) xb[t] = qkv[(size_t)min(t, n - 1) * ldp + ch];
 #pragma unroll
-      for (int o = 0; o < GDN_SPLIT; ++o)
-        v[o] = __hip_atomic_load(&gdn_xchg[j][t][o], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      done = true;
+  for (int q = 0; q < 3; ++q) hb[q] = ring[(size_t)((P - 3 + q) & (GDN_RING - 1)) * C + ch];
+  const int gt = tid - GDN_D;
+  const int gtc = min(max(gt, 0), n - 1);
+  const __bf16 bb = b[(size_t)gtc * ldp + j], ab = a[(size_t)gtc * ldp + j];
+  const __bf16 dtb = dt_bias[j], alb = A_log[j];
+  // outputs, z and weights of rows w and w + 4, columns 2 lane, 2 lane + 1
+  __bf16 ob[2][2], zb[2][2];
 #pragma unroll
-      for (int o = 0; o < GDN_SPLIT; ++o) done = done && (unsigned)(v[o] >> 32) == tag;
-      if (!done) __builtin_amdgcn_s_sleep(1);
+  for (int h = 0; h < 2; ++h) {
+    const int t = min(w + 4 * h, n - 1);
+    const __bf16* src = out + (size_t)t * ldo + j * GDN_D + 2 * lane;
+    const __bf16* zp = z + (size_t)t * ldp + j * GDN_D + 2 * lane;
+    ob[h][0] = src[0];
+    ob[h][1] = src[1];
+    zb[h][0] = zp[0];
+    zb[h][1] = zp[1];
+  }
+  const float nw0 = bf16_to_f32(norm_w[2 * lane]), nw1 = bf16_to_f32(norm_w[2 * lane + 1]);
+
+  float y[GDN_MAXN];
+  if (tid < GDN_D) {
+    const float cw[4] = {lo_bf16(wk.x), hi_bf16(wk.x), lo_bf16(wk.y), hi_bf16(wk.y)};
+    float xs[3 + GDN_MAXN];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) xs[q] = P - 3 + q >= 0 ? bf16_to_f32(hb[q]) : 0.f;
+#pragma unroll
+    for (int t = 0; t < GDN_MAXN; ++t) xs[3 + t] = bf16_to_f32(xb[t]);
+#pragma unroll
+    for (int t = 0; t < GDN_MAXN; ++t) {
+      y[t] = 0.f;
+      if (t < n) {
+        y[t] = conv_silu(cw, xs, t);
+        const float ss = wave_sum_fast(y[t] * y[t]);
+        if (lane == 0) l2p[t][w] = ss;
+      }
     }
-    float tot = 0.f;
+  }
 #pragma unroll
-    for (int o = 0; o < GDN_SPLIT; ++o) tot += __uint_as_float((unsigned)v[o]);
-    sst[t] = done ? tot : __int_as_float(0x7fc00000);
+  for (int h = 0; h < 2; ++h) {
+    oa[w + 4 * h][2 * lane] = bf16_to_f32(ob[h][0]);
+    oa[w + 4 * h][2 * lane + 1] = bf16_to_f32(ob[h][1]);
   }
   __syncthreads();
-
-  // ---- gated RMSNorm of this workgroup's columns: thread = (row ot, column cb + oc) ----
-  if (qk_thread && ot < n) {
-    const float inv = 1.0f / sqrtf(sst[ot] / 128.0f + eps);
-    const float y = round_bf16(bf16_to_f32(nwb) * round_bf16(oa[ot][oc] * inv));
-    out[(size_t)ot * ldo + j * GDN_D + cb + oc] = f32_to_bf16(y * silu_f(bf16_to_f32(zb)));
+  if (tid < GDN_D) {
+#pragma unroll
+    for (int t = 0; t < GDN_MAXN; ++t) {
+      if (t < n) {
+        const float inv = 1.0f / sqrtf((l2p[t][0] + l2p[t][1]) + 1e-6f);
+        st_k[((size_t)t * Hv + j) * GDN_D + c] = y[t] * inv;
+      }
+    }
   }
-  // Stage the normalised k rows and the gates (part 0 of the head). Only now: every part has
-  // published its partial sum, which it does after its own loads of the previous call's staged
-  // rows at these addresses have returned.
-  if (g == 0 && qk_thread) {
-    for (int t = part; t < n; t += 2) st_k[((size_t)t * Hv + j) * GDN_D + c] = ka[t][c];
-    if (tid < n)
-      *reinterpret_cast<float2*>(st_g + ((size_t)tid * Hv + j) * 2) =
-          make_float2(ga[tid][0], ga[tid][1]);
+  if (gt >= 0 && gt < n)
+    *reinterpret_cast<float2*>(st_g + ((size_t)gt * Hv + j) * 2) = gate_values(bb, ab, dtb, alb);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int t = w + 4 * h;
+    if (t < n)
+      gated_norm_row(oa[t], lane, nw0, nw1, bf16_to_f32(zb[h][0]), bf16_to_f32(zb[h][1]), eps,
+                     out + (size_t)t * ldo + j * GDN_D);
   }
 }
 
 }  // namespace qe
 
 using namespace qe;
-
-// Compute units of the current device, queried once per device (0 if the query fails).
-static int device_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cus[dev] == 0) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cus[dev] = v;
-  }
-  return cus[dev];
-}
 
 extern "C" hipError_t qe_gdn_step_n(const void* qkv, const void* z, const void* b, const void* a,
                                     long ldp, void* ring, const void* conv_w, const void* A_log,
@@ -588,17 +615,26 @@ extern "C" hipError_t qe_gdn_step_n(const void* qkv, const void* z, const void* 
   if (C >= (1L << 26) || ldp < C || ldo < (long)Hv * GDN_D) return hipErrorInvalidValue;
   if (!al(S, 16) || !al(st_k, 16) || !al(st_v, 16) || !al(st_g, 8) || !al(conv_w, 8))
     return hipErrorInvalidValue;
-  // 2-8 rows: the split kernel when its whole grid fits at once; 1 row (the split gains nothing
-  // there: the exchange costs what the spread saves) and larger grids: one workgroup per head.
-  // Both give the same bits.
-  if (n >= 2 && Hv <= GDN_SPLIT_MAX_HV && Hv * GDN_SPLIT <= device_cus()) {
+  // 5-8 rows: the split kernel and its finish kernel; 1-4 rows: one workgroup per head (below
+  // five rows the split's second launch costs more than the spread saves: same-box A/B on
+  // MI355X at Hk 16 / Hv 48, 2 rows 11.2 vs 9.5 us, 4 rows 12.9 vs 12.6, 6 rows 15.4 vs 15.7,
+  // 8 rows 17.4 vs 18.8). Both paths give the same bits.
+  if (n >= GDN_SPLIT_MIN_ROWS) {
     gdn_split_kernel<GDN_SPLIT_THREADS><<<dim3(Hv * GDN_SPLIT), dim3(GDN_SPLIT_THREADS), 0, stream>>>(
+        static_cast<const __bf16*>(qkv), static_cast<const __bf16*>(b),
+        static_cast<const __bf16*>(a), ldp, static_cast<__bf16*>(ring),
+        static_cast<const __bf16*>(conv_w), static_cast<const __bf16*>(A_log),
+        static_cast<const __bf16*>(dt_bias), S, st_k, st_v, st_g, ctl, static_cast<__bf16*>(out),
+        ldo, n, Hk, Hv);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    gdn_finish_kernel<<<dim3(Hv), dim3(256), 0, stream>>>(
         static_cast<const __bf16*>(qkv), static_cast<const __bf16*>(z),
         static_cast<const __bf16*>(b), static_cast<const __bf16*>(a), ldp,
-        static_cast<__bf16*>(ring), static_cast<const __bf16*>(conv_w),
+        static_cast<const __bf16*>(ring), static_cast<const __bf16*>(conv_w),
         static_cast<const __bf16*>(A_log), static_cast<const __bf16*>(dt_bias),
-        static_cast<const __bf16*>(norm_w), S, st_k, st_v, st_g, ctl, static_cast<__bf16*>(out),
-        ldo, n, Hk, Hv, eps);
+        static_cast<const __bf16*>(norm_w), st_k, st_g, ctl, static_cast<__bf16*>(out), ldo, n,
+        Hk, Hv, eps);
     return hipGetLastError();
   }
   gdn_step_kernel<<<dim3(Hv), dim3(GDN_THREADS), 0, stream>>>(

@@ -7,7 +7,8 @@ reference's own tests (tests/test_kernels.py:165-286 of the reference):
     committed state;
   * NaN in one head stays in that head;
 plus the staged rows and the conv ring against the oracle, graph replays against eager calls,
-the C ABI against the torch op, and the reference's q switch having no effect."""
+the C ABI against the torch op, concurrent calls on two streams against sequential ones, and the
+reference's q switch having no effect."""
 import pytest
 import torch
 
@@ -90,8 +91,8 @@ def close(out, ref):
     return ok and frac < 0.01, d.max().item(), frac
 
 
-# 2-8 rows at Hv <= 64 run the split kernel (4 workgroups per head, partial sums exchanged between
-# them); 1 row, Hv = 72 and Hv = 264 run the one-workgroup-per-head kernel.
+# 5-8 rows run the split kernel (4 workgroups per head) and its finish kernel, 1-4 rows the
+# one-workgroup-per-head kernel; Hv = 264 makes a split grid of 1,056 workgroups, more than the CUs.
 @pytest.mark.parametrize("hk,hv", [(16, 48), (16, 16), (2, 2), (1, 3), (9, 72), (8, 264)])
 def test_gdn_step_n_vs_oracle(native, hk, hv):
     W = weights(hk, hv, seed=hk + hv)
@@ -140,30 +141,34 @@ def test_gdn_nan_isolated_to_head(native, col):
     assert not torch.isnan(out[0, :128]).any()
 
 
-def test_split_and_single_kernels_agree(native):
-    """A 72-head layer (always the one-workgroup kernel) and its first 64 heads as a layer of
-    their own (the split kernel for 2-8 rows, the one-workgroup kernel for 1 row), both with 8
-    value heads per qk head, give the same state and the same outputs bit for bit: the kernels
-    share the per-column arithmetic and the RMSNorm's summation order, which is what lets a call
-    pick either."""
-    hkb, hvb, hks, hvs = 9, 72, 8, 64
-    W_big = weights(hkb, hvb, seed=21)
-    D = 128
-    # the small layer's channels: q and k of the first 8 qk heads, v of the first 64 heads
-    chans = (list(range(hks * D)) + list(range(hkb * D, hkb * D + hks * D))
-             + list(range(2 * hkb * D, 2 * hkb * D + hvs * D)))
-    W_small = {"conv_w": W_big["conv_w"][chans], "A_log": W_big["A_log"][:hvs],
-               "dt_bias": W_big["dt_bias"][:hvs], "norm_w": W_big["norm_w"]}
-    big, small = gpu_layer(native, hkb, hvb, W_big), gpu_layer(native, hks, hvs, W_small)
-    idx = torch.tensor(chans, device=DEV)
-    for it, (n, kp) in enumerate([(3, 2), (8, 8), (1, 1), (5, 3), (2, 1), (1, 1)]):
-        rb = make_rows(hkb, hvb, n, seed=70 + it)
-        qkv, z, b, a = big.views(rb)
-        rs = torch.cat([qkv[:, idx], z[:, :hvs * D], b[:, :hvs], a[:, :hvs]], dim=1)
-        ob, os_ = big.run(rb, kp), small.run(rs, kp)
-        assert torch.equal(big.S[:hvs], small.S), it
-        assert torch.equal(ob[:, :hvs * D], os_), it
-    assert hvb // hkb == hvs // hks == 8
+def test_concurrent_calls_on_two_streams(native):
+    """Two layers stepped at the same time on two streams, 5-8-row calls (the split kernel and its
+    finish kernel) among them, give the outputs and states of the same calls made one after the
+    other: a call keeps no state outside the caller's buffers, so calls on different layers may
+    overlap."""
+    hk, hv = 16, 48
+    WA, WB = weights(hk, hv, seed=31), weights(hk, hv, seed=32)
+    plan = [(4, 2), (8, 8), (1, 1), (6, 3), (2, 2), (8, 5), (3, 3)]
+    rows_a = [make_rows(hk, hv, n, seed=200 + i) for i, (n, _) in enumerate(plan)]
+    rows_b = [make_rows(hk, hv, n, seed=300 + i) for i, (n, _) in enumerate(plan)]
+    ref_a, ref_b = gpu_layer(native, hk, hv, WA), gpu_layer(native, hk, hv, WB)
+    want = [(ref_a.run(ra, k), ref_b.run(rb, k)) for (_, k), ra, rb in zip(plan, rows_a, rows_b)]
+    A, B = gpu_layer(native, hk, hv, WA), gpu_layer(native, hk, hv, WB)
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    got = []
+    for (_, k), ra, rb in zip(plan, rows_a, rows_b):
+        with torch.cuda.stream(sa):
+            oa = A.run(ra, k)
+        with torch.cuda.stream(sb):
+            ob = B.run(rb, k)
+        got.append((oa, ob))
+    torch.cuda.synchronize()
+    for it, ((wa, wb), (ga, gb)) in enumerate(zip(want, got)):
+        assert torch.equal(ga, wa) and torch.equal(gb, wb), it
+    assert torch.equal(A.S, ref_a.S) and torch.equal(B.S, ref_b.S)
+    for x, y in zip(A.st + B.st + [A.ring, B.ring], ref_a.st + ref_b.st + [ref_a.ring, ref_b.ring]):
+        assert torch.equal(x, y)
 
 
 def test_staged_rows_and_ring_match_the_oracle(native):
