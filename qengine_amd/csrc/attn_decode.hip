@@ -1157,7 +1157,7 @@ extern "C" hipError_t qe_attn_decode_noalloc(const void* q, const void* kc, cons
 }
 
 static bool kv_scales_ok(float k_scale, float v_scale) {
-  return k_scale > 0.f && v_scale > 0.f && k_scale < INFINITY && v_scale < INFINITY;
+  return kv_scale_ok(k_scale) && kv_scale_ok(v_scale);
 }
 
 extern "C" hipError_t qe_attn_decode_fp8_partials(const void* q, const void* kc8, const void* vc8,

@@ -337,7 +337,7 @@ extern "C" hipError_t qe_attn_prefill_fp8(const void* q, const void* kc8, const 
                                           long ldo, int T, int Hq, int Hkv, int max_len,
                                           float scale, float k_scale, float v_scale,
                                           hipStream_t stream) {
-  if (!(k_scale > 0.f) || !(v_scale > 0.f) || k_scale == INFINITY || v_scale == INFINITY)
+  if (!kv_scale_ok(k_scale) || !kv_scale_ok(v_scale))
     return hipErrorInvalidValue;
   return launch_prefill(q, kc8, vc8, pos, qg, ldp, out, ldo, T, Hq, Hkv, max_len, scale, true,
                         k_scale, v_scale, stream);

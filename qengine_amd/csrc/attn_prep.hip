@@ -140,7 +140,7 @@ extern "C" hipError_t qe_attn_prep_fp8(const void* qg, const void* k, const void
                                        float k_scale, float v_scale, hipStream_t stream) {
   if (!prep_args_ok(qg, k, v, ldp, qnw, knw, inv_freq, pos, q_out, kc8, vc8, n, Hq, Hkv, max_len,
                     rd) ||
-      !(k_scale > 0.f) || !(v_scale > 0.f) || k_scale == INFINITY || v_scale == INFINITY)
+      !kv_scale_ok(k_scale) || !kv_scale_ok(v_scale))
     return hipErrorInvalidValue;
   launch_prep<true>(qg, k, v, ldp, qnw, knw, inv_freq, pos, q_out, kc8, vc8, n, Hq, Hkv, max_len,
                     rd, eps, 1.0f / k_scale, 1.0f / v_scale, stream);

@@ -10,6 +10,7 @@
 // The _check_* functions run the same validation without the device requirement and without a
 // launch, so the contract can be exercised on a machine without a GPU.
 #include <cmath>
+#include <limits>
 
 #include <torch/extension.h>
 #include <c10/core/DeviceGuard.h>
@@ -102,6 +103,7 @@ PrepArgs parse_prep(const torch::Tensor& qg, const torch::Tensor& k, const torch
   const int n = QG.n, Hkv = kc.size(0), max_len = kc.size(1), Hq = QO.w / HD;
   TORCH_CHECK(n >= 1 && n <= max_rows && K.n == n && V.n == n && QO.n == n && QO.ld == QO.w,
               "prep takes 1..", max_rows, " rows, equal in every argument, and contiguous q_out rows");
+  TORCH_CHECK(QO.w == (long)Hq * HD, "q_out width must be Hq*256");
   TORCH_CHECK(Hq >= 1 && QG.w == (long)Hq * 2 * HD && K.w == (long)Hkv * HD &&
                   V.w == (long)Hkv * HD,
               "row widths must be qg = Hq*512, k = v = Hkv*256");
@@ -140,6 +142,7 @@ DecodeArgs parse_decode(const torch::Tensor& q, const torch::Tensor& kc, const t
   const int n = Qr.n, Hq = Qr.w / HD, Hkv = kc.size(0), max_len = kc.size(1);
   TORCH_CHECK(Hq >= 1 && Qr.ld == Qr.w && QG.n == n && O.n == n && Hq % Hkv == 0,
               "q rows must be contiguous, rows must agree and Hq % Hkv == 0");
+  TORCH_CHECK(Qr.w == (long)Hq * HD, "q width must be Hq*256");
   TORCH_CHECK(part_o.dim() == 4 && part_o.size(0) >= n && part_o.size(1) == Hq &&
                   part_o.size(3) == HD,
               "part_o must be [>=n, Hq, NS, 256]");
@@ -181,13 +184,25 @@ void attn_prep_chunk(torch::Tensor qg, torch::Tensor k, torch::Tensor v, torch::
 }
 
 // Chunked prefill: q [T, Hq*256] contiguous (normed + roped), kc/vc [Hkv, max_len, 256] holding
-// the chunk's K/V, qg rows [T, >= Hq*512] (gate source), out rows [T, Hq*256].
-void attn_prefill(torch::Tensor q, torch::Tensor kc, torch::Tensor vc, torch::Tensor pos,
-                  torch::Tensor qg, torch::Tensor out) {
-  auto Qr = rows(q, BF, "q", true), QG = rows(qg, BF, "qg", true), O = rows(out, BF, "out", true);
-  chk(kc, BF, "kc", true);
-  chk(vc, BF, "vc", true);
-  chk_pos(pos, true);
+// the chunk's K/V (bf16, or E4M3FN codes with kv8), qg rows [T, >= Hq*512] (gate source), out
+// rows [T, Hq*256].
+struct PrefillArgs {
+  int T, Hq, Hkv, max_len;
+  long ldp, ldo;
+};
+
+PrefillArgs parse_prefill(const torch::Tensor& q, const torch::Tensor& kc, const torch::Tensor& vc,
+                          const torch::Tensor& pos, const torch::Tensor& qg,
+                          const torch::Tensor& out, bool dev, bool kv8 = false) {
+  auto Qr = rows(q, BF, "q", dev), QG = rows(qg, BF, "qg", dev), O = rows(out, BF, "out", dev);
+  if (kv8) {
+    chk_kv8(kc, "kc8", dev);
+    chk_kv8(vc, "vc8", dev);
+  } else {
+    chk(kc, BF, "kc", dev);
+    chk(vc, BF, "vc", dev);
+  }
+  chk_pos(pos, dev);
   chk16(q, Qr.ld, "q");
   chk16(qg, QG.ld, "qg");
   chk16(out, O.ld, "out");
@@ -198,11 +213,18 @@ void attn_prefill(torch::Tensor q, torch::Tensor kc, torch::Tensor vc, torch::Te
   const int T = Qr.n, Hq = Qr.w / HD, Hkv = kc.size(0), max_len = kc.size(1);
   TORCH_CHECK(Hq >= 1 && Qr.ld == Qr.w && QG.n == T && O.n == T && Hq % Hkv == 0,
               "q rows must be contiguous, rows must agree and Hq % Hkv == 0");
+  TORCH_CHECK(Qr.w == (long)Hq * HD, "q width must be Hq*256");
   TORCH_CHECK(O.w == (long)Hq * HD && QG.w >= (long)Hq * 2 * HD, "out width Hq*256; qg width Hq*512");
+  return {T, Hq, Hkv, max_len, QG.ld, O.ld};
+}
+
+void attn_prefill(torch::Tensor q, torch::Tensor kc, torch::Tensor vc, torch::Tensor pos,
+                  torch::Tensor qg, torch::Tensor out) {
+  const auto a = parse_prefill(q, kc, vc, pos, qg, out, true);
   const c10::DeviceGuard guard(q.device());
   raise_on(qe_attn_prefill(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), pos.data_ptr<int>(),
-                           qg.data_ptr(), QG.ld, out.data_ptr(), O.ld, T, Hq, Hkv, max_len,
-                           1.0f / 16.0f, stream_of(q)),
+                           qg.data_ptr(), a.ldp, out.data_ptr(), a.ldo, a.T, a.Hq, a.Hkv,
+                           a.max_len, 1.0f / 16.0f, stream_of(q)),
            "qe_attn_prefill");
 }
 
@@ -291,8 +313,13 @@ std::vector<int64_t> check_attn_decode(torch::Tensor q, torch::Tensor kc, torch:
 // attn_prep / attn_decode over a cache of E4M3FN codes with per-cache scales: a stored code c
 // means c * scale; prep stores round-to-nearest-even(x / scale), saturated at +-448.
 void kv_scales(double k_scale, double v_scale) {
-  TORCH_CHECK(k_scale > 0 && v_scale > 0 && std::isfinite(k_scale) && std::isfinite(v_scale),
-              "k_scale and v_scale must be positive and finite");
+  // as fp32, the kernels' type: normal and finite, so that 1/scale is finite too
+  const auto ok = [](double s) {
+    const float f = (float)s;
+    return f >= std::numeric_limits<float>::min() && f <= std::numeric_limits<float>::max();
+  };
+  TORCH_CHECK(ok(k_scale) && ok(v_scale),
+              "k_scale and v_scale must be positive, finite and not subnormal as fp32");
 }
 
 void attn_prep_fp8(torch::Tensor qg, torch::Tensor k, torch::Tensor v, torch::Tensor qnw,
@@ -314,26 +341,13 @@ void attn_prep_fp8(torch::Tensor qg, torch::Tensor k, torch::Tensor v, torch::Te
 // attn_prefill over the fp8 cache (kc8/vc8 [Hkv, max_len, 256] E4M3FN codes).
 void attn_prefill_fp8(torch::Tensor q, torch::Tensor kc8, torch::Tensor vc8, torch::Tensor pos,
                       torch::Tensor qg, torch::Tensor out, double k_scale, double v_scale) {
-  auto Qr = rows(q, BF, "q", true), QG = rows(qg, BF, "qg", true), O = rows(out, BF, "out", true);
-  chk_kv8(kc8, "kc8", true);
-  chk_kv8(vc8, "vc8", true);
-  chk_pos(pos, true);
   kv_scales(k_scale, v_scale);
-  chk16(q, Qr.ld, "q");
-  chk16(qg, QG.ld, "qg");
-  chk16(out, O.ld, "out");
-  chk16(kc8, HD, "kc8");
-  chk16(vc8, HD, "vc8");
-  TORCH_CHECK(kc8.dim() == 3 && kc8.size(2) == HD && vc8.sizes() == kc8.sizes(),
-              "kc8/vc8 must be [Hkv, max_len, 256] with equal sizes");
-  const int T = Qr.n, Hq = Qr.w / HD, Hkv = kc8.size(0), max_len = kc8.size(1);
-  TORCH_CHECK(Hq >= 1 && Qr.ld == Qr.w && QG.n == T && O.n == T && Hq % Hkv == 0,
-              "q rows must be contiguous, rows must agree and Hq % Hkv == 0");
-  TORCH_CHECK(O.w == (long)Hq * HD && QG.w >= (long)Hq * 2 * HD, "out width Hq*256; qg width Hq*512");
+  const auto a = parse_prefill(q, kc8, vc8, pos, qg, out, true, true);
   const c10::DeviceGuard guard(q.device());
   raise_on(qe_attn_prefill_fp8(q.data_ptr(), kc8.data_ptr(), vc8.data_ptr(), pos.data_ptr<int>(),
-                               qg.data_ptr(), QG.ld, out.data_ptr(), O.ld, T, Hq, Hkv, max_len,
-                               1.0f / 16.0f, (float)k_scale, (float)v_scale, stream_of(q)),
+                               qg.data_ptr(), a.ldp, out.data_ptr(), a.ldo, a.T, a.Hq, a.Hkv,
+                               a.max_len, 1.0f / 16.0f, (float)k_scale, (float)v_scale,
+                               stream_of(q)),
            "qe_attn_prefill_fp8");
 }
 
@@ -656,6 +670,15 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "validate attn_prep_decode arguments without launching");
   m.def("_check_attn_decode", &check_attn_decode,
         "validate attn_decode arguments without launching");
+  m.def("_check_attn_prefill",
+        [](torch::Tensor q, torch::Tensor kc, torch::Tensor vc, torch::Tensor pos, torch::Tensor qg,
+           torch::Tensor out, bool kv8) {
+          const auto a = parse_prefill(q, kc, vc, pos, qg, out, false, kv8);
+          return std::vector<int64_t>{a.T, a.Hq, a.Hkv, a.max_len, a.ldp, a.ldo};
+        },
+        "validate attn_prefill (kv8: attn_prefill_fp8) arguments without launching");
+  m.def("_check_kv_scales", [](double k, double v) { kv_scales(k, v); },
+        "validate the fp8 cache scales of the *_fp8 ops");
   m.def("gemv_bf16", &gemv_bf16, "out[n, N] = x[n, K] @ W[N, K]^T, n = 1..8 (W, x, out)");
   m.def("attn_prep_fp8", &attn_prep_fp8,
         "attn_prep writing the fp8 KV cache (qg, k, v, qnw, knw, inv_freq, pos, q_out, kc8, vc8, "

@@ -204,6 +204,13 @@ __device__ __forceinline__ u32x4_t fp8x8_to_bf16x8(u32x2_t w) {
                  fp8x2_to_bf16x2_hi(w[1])};
 }
 
+// A usable per-cache scale: a normal, finite fp32 value (NaN fails both comparisons). Subnormal
+// scales are rejected because their fp32 reciprocal, the encoder's multiplier, overflows to inf,
+// which would turn zero inputs into NaN codes.
+__host__ __device__ inline bool kv_scale_ok(float s) {
+  return s >= 1.17549435e-38f && s <= 3.40282347e38f;
+}
+
 // x -> fp8 code: round to nearest even, saturate at +-448, NaN stays NaN.
 __device__ __forceinline__ uint8_t f32_to_fp8(float x) {
   const float c = x != x ? x : fminf(fmaxf(x, -448.0f), 448.0f);

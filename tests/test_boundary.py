@@ -109,11 +109,34 @@ def test_capi_prefill_rejects(capi, fp8, kw, why):
     assert r == INVALID, why
 
 
-@pytest.mark.parametrize("ks,vs", [(0.0, 1.0), (1.0, -1.0), (float("inf"), 1.0), (1.0, float("nan"))])
-def test_capi_prefill_fp8_rejects_scales(capi, ks, vs):
-    r = capi.load().qe_attn_prefill_fp8(A, A, A, A, A, 48 * D, A, 24 * D, 16, 24, 4, 4096, 1.0 / 16,
-                                        ks, vs, None)
-    assert r == INVALID
+BAD_SCALES = [(0.0, 1.0), (1.0, -1.0), (float("inf"), 1.0), (1.0, float("nan")),
+              (1e-39, 1.0), (1.0, 1e-45)]  # the last two: subnormal, 1/scale overflows to inf
+
+
+@pytest.mark.parametrize("ks,vs", BAD_SCALES)
+def test_capi_fp8_ops_reject_scales(capi, ks, vs):
+    """Every fp8-cache entry point rejects scales that are not normal finite fp32 values."""
+    lib = capi.load()
+    assert lib.qe_attn_prefill_fp8(A, A, A, A, A, 48 * D, A, 24 * D, 16, 24, 4, 4096, 1.0 / 16,
+                                   ks, vs, None) == INVALID
+    assert lib.qe_attn_prep_fp8(A, A, A, 48 * D + 2048, A, A, A, A, A, A, A, 1, 24, 4, 4096, 64,
+                                1e-6, ks, vs, None) == INVALID
+    assert lib.qe_attn_decode_fp8(A, A, A, A, A, 48 * D, A, A, A, 24 * D, 1, 24, 4, 4096, 16,
+                                  1.0 / 16, ks, vs, None) == INVALID
+    if not 1.17549435e-38 <= ks <= 3.4028235e38:  # the partials take k_scale only
+        assert lib.qe_attn_decode_fp8_partials(A, A, A, A, A, A, 1, 24, 4, 4096, 16, 1.0 / 16, ks,
+                                               None) == INVALID
+
+
+@pytest.mark.parametrize("ks,vs", BAD_SCALES)
+def test_fp8_ops_contract_rejects_scales(native, ks, vs):
+    with pytest.raises(RuntimeError, match="not subnormal"):
+        native._check_kv_scales(ks, vs)
+
+
+def test_fp8_ops_contract_accepts_normal_scales(native):
+    for ks, vs in ((1.0 / 16, 1.0 / 16), (1.17549435e-38, 3.0e38), (448.0, 1e-3)):
+        native._check_kv_scales(ks, vs)
 
 
 @pytest.mark.parametrize("kw,why", [
@@ -205,6 +228,7 @@ def _mut(**changes):
     (_mut(vc=lambda a: torch.zeros(4, 32, D, dtype=BF)), "equal sizes"),
     (_mut(kc=lambda a: torch.zeros(4, 64, 128, dtype=BF), vc=lambda a: torch.zeros(4, 64, 128, dtype=BF)),
      "256"),
+    (_mut(q=lambda a: torch.zeros(2, 24 * D + 8, dtype=BF)), "q width must be Hq"),
 ])
 def test_decode_contract_rejects(native, mutate, msg):
     a = mutate(decode_args())
@@ -255,10 +279,37 @@ def test_prep_contract_accepts_engine_layout(native):
     (_mut(vc=lambda a: torch.zeros(4, 65, D, dtype=BF)), "vc must match"),
     (_mut(inv_freq=lambda a: torch.zeros(129, dtype=F32)), "<= 256"),
     (_mut(q_out=lambda a: torch.zeros(2, 25 * D, dtype=BF)), "row widths"),
+    (_mut(q_out=lambda a: torch.zeros(2, 24 * D + 8, dtype=BF)), "q_out width must be Hq"),
 ])
 def test_prep_contract_rejects(native, mutate, msg):
     with pytest.raises(RuntimeError, match=msg):
         check_prep(native, mutate(prep_args()))
+
+
+def prefill_args(T=16, hq=24, hkv=4, max_len=64, kv8=False, pad=8):
+    kdt = torch.float8_e4m3fn if kv8 else BF
+    return dict(q=torch.zeros(T, hq * D, dtype=BF), kc=torch.zeros(hkv, max_len, D, dtype=kdt),
+                vc=torch.zeros(hkv, max_len, D, dtype=kdt), pos=torch.zeros(1, dtype=I32),
+                qg=torch.zeros(T, hq * 2 * D + pad, dtype=BF)[:, : hq * 2 * D],
+                out=torch.zeros(T, hq * D, dtype=BF))
+
+
+def check_prefill(C, a, kv8=False):
+    return C._check_attn_prefill(a["q"], a["kc"], a["vc"], a["pos"], a["qg"], a["out"], kv8)
+
+
+@pytest.mark.parametrize("kv8", [False, True])
+def test_prefill_contract(native, kv8):
+    T, hq, hkv, max_len, ldp, ldo = check_prefill(native, prefill_args(kv8=kv8), kv8)
+    assert (T, hq, hkv, max_len, ldp, ldo) == (16, 24, 4, 64, 24 * 2 * D + 8, 24 * D)
+    for mutate, msg in [
+            (_mut(q=lambda a: torch.zeros(16, 24 * D + 8, dtype=BF)), "q width must be Hq"),
+            (_mut(q=lambda a: torch.zeros(16, 24 * D + 8, dtype=BF)[:, : 24 * D]), "contiguous"),
+            (_mut(out=lambda a: torch.zeros(15, 24 * D, dtype=BF)), "rows must agree"),
+            (_mut(qg=lambda a: torch.zeros(16, 24 * D, dtype=BF)), "qg width"),
+            (_mut(vc=lambda a: a["vc"][:, :32].contiguous()), "equal sizes")]:
+        with pytest.raises(RuntimeError, match=msg):
+            check_prefill(native, mutate(prefill_args(kv8=kv8)), kv8)
 
 
 def test_prep_contract_row_limit(native):
