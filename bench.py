@@ -150,6 +150,7 @@ def capture(torch, fn):
 
 
 MIN_WARMUP_REPLAYS = 30  # the reference's time_graph warms each graph up 30 times
+MIN_WARMUP_SECONDS = 0.1  # and at least this long per graph: clocks ramp over tens of ms
 
 
 class Timing:
@@ -167,11 +168,15 @@ class Timing:
 
 def time_graphs(torch, graphs, steps: int, warmup: int) -> Timing:
     """The reference's graph timing (bench/engine/micro_kernels.py:16-32): at least 30 warm-up
-    replays, then ``steps`` timed replays (graphs round-robin), each bracketed by events on the
-    current stream, the one the graphs' kernels run on."""
-    for i in range(max(warmup, MIN_WARMUP_REPLAYS)):
-        graphs[i % len(graphs)].replay()
-    torch.cuda.synchronize()
+    replays (and at least MIN_WARMUP_SECONDS of them), then ``steps`` timed replays (graphs
+    round-robin), each bracketed by events on the current stream, the one the graphs' kernels
+    run on."""
+    t0, i = time.perf_counter(), 0
+    while i < max(warmup, MIN_WARMUP_REPLAYS) or time.perf_counter() - t0 < MIN_WARMUP_SECONDS:
+        for _ in range(10):
+            graphs[i % len(graphs)].replay()
+            i += 1
+        torch.cuda.synchronize()
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     ev[0].record()
     for i in range(steps):
@@ -741,6 +746,9 @@ def main():
                     help="only the Gated DeltaNet step at the model's shapes, as JSON")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the in_proj / o_proj GEMV and the HBM read probe, as JSON")
+    ap.add_argument("--sweep-only", action="store_true",
+                    help="only the decode sweep over exactly --lengths (one JSON object per "
+                         "length); the per-length runs that rocprofv3 profiles")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other BASELINE configs (1, 3, 4, 5)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -768,6 +776,7 @@ def main():
     import qengine_amd as qa
     C = qa._C
     torch.backends.cuda.matmul.allow_tf32 = False
+    warm_s = warm_device(torch)
     if args.prefill_only:
         print(json.dumps(bench_prefill(torch, C, args.steps, args.warmup)))
         return
@@ -786,9 +795,14 @@ def main():
         print(json.dumps(bench_gdn(torch, C, args.steps, args.warmup)))
         return
     lengths = [int(x) for x in args.lengths.split(",") if x]
+    if args.sweep_only:
+        for L in lengths:
+            r = bench_length(torch, C, qa, L, args.steps, args.warmup, args.ns or None)
+            print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
+                              for k, v in r.items()}), flush=True)
+        return
     if HEADLINE_L not in lengths:
         lengths.append(HEADLINE_L)
-    warm_s = warm_device(torch)
     node_us = launch_floor_us(torch, args.steps, args.warmup)
     print(f"# warm-up {warm_s:.2f} s; empty graph node {node_us:.2f} us", file=sys.stderr,
           flush=True)
