@@ -697,9 +697,12 @@ constexpr int TILE_U4 = TILE * ROW_CHUNKS;   // 16-byte slots of one K (or V) ti
 constexpr int REGION_U4 = 2 * TILE_U4;       // a subset's K tile then V tile
 }  // namespace cols
 
-// KV8: an fp8 cache (E4M3FN codes). The subset's K tile goes to LDS in the swizzled 256-byte-row
-// layout of load_tile8 (read by qk_tile8), its V tile row-major; both are 8 KB and convert to the
-// same bf16 operands exactly, so the tile arithmetic below is unchanged.
+// KV8: an fp8 cache (E4M3FN codes). The subset's 8 KB fp8 K and V tiles land row-major in its
+// 16 KB bf16 V region (K, then V); its waves convert them once (exactly: every E4M3 value is a
+// bf16 value) into the bf16 K and V tiles, laid out and swizzled as the bf16 path loads them, and
+// the tile arithmetic below runs unchanged. So with scales of 1 the result equals the bf16
+// kernel's on the dequantized cache, bit for bit. Converting once instead of in every wave that
+// reads a tile took the 8-row verify from 17.1 to 14.6 us (partials, 4k) and 29.0 to 25.2 (16k).
 template <int NT, int CPW, bool KV8 = false>
 __global__ void __launch_bounds__(cols::SUBSETS * (NT / CPW) * WAVE)
 attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
@@ -746,7 +749,7 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
   constexpr int ELEM = KV8 ? 1 : 2;  // bytes per cache value
   const size_t head_off = (size_t)g * max_len * HD * ELEM;  // bytes
   u32x4_t* kt = lds + sub * cols::REGION_U4;
-  const u32x4_t* vt = kt + (KV8 ? cols::TILE_U4 / 2 : cols::TILE_U4);
+  u32x4_t* vt = kt + cols::TILE_U4;
 
   // One pass, inlined once per call of the lambda (a loop over passes would keep the merge's
   // loop-invariant addresses live through the tile rounds and spill).
@@ -763,7 +766,7 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
         make_rsrc_uniform(reinterpret_cast<const char*>(vc) + head_off, bytes);
 
     float m[CPW], l[CPW];
-    f32x4_t acc[CPW][16];  // bf16: tile::pv_tile_tr layout; fp8: tile::pv_half layout
+    f32x4_t acc[CPW][16];  // tile::pv_tile_tr layout
 #pragma unroll
     for (int u = 0; u < CPW; ++u) {
       m[u] = -INFINITY;
@@ -778,16 +781,12 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
       const int p0 = P.beg + (r * SUB + sub) * TILE;  // this subset's tile in round r
       const bool has = p0 < P.end;                     // uniform per subset
       if (has && KV8) {
-        // fp8: 8 loads of K (rows 4j .. 4j+3, chunks swizzled as in load_tile8) and 8 of V
-        // (row-major), one KB each, shared by the subset's waves.
+        // fp8: 8 loads of K then 8 of V, one KB (rows 4j .. 4j+3) each, shared by the subset's
+        // waves: 16-byte chunk q of row r of K at vt[16 r + q], of V at vt[512 + 16 r + q].
         for (int i = rank; i < 16; i += WPS) {
-          const int j = i & 7, row = 4 * j + (lane >> 4);
-          if (i < 8)
-            buffer_load16_to_lds(krs, (uint32_t)(p0 + row) * HD + ((lane & 15) ^ (row & 15)) * 16,
-                                 kt + 64 * j);
-          else
-            buffer_load16_to_lds(vrs, (uint32_t)(p0 + row) * HD + (lane & 15) * 16,
-                                 kt + cols::TILE_U4 / 2 + 64 * j);
+          const int row = 4 * (i & 7) + (lane >> 4);
+          buffer_load16_to_lds(i < 8 ? krs : vrs, (uint32_t)(p0 + row) * HD + (lane & 15) * 16,
+                               vt + 64 * i);
         }
       } else if (has) {
         // The subset's WPS waves share its 32 LDS-DMA loads: 16 of K (rows 2i, 2i+1, swizzled as
@@ -804,31 +803,55 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
       }
       vmcnt_wait<0>();
       __syncthreads();  // every wave's loads of this round have landed
+      if constexpr (KV8) {
+        // Convert once: thread (rank, lane) takes fp8 chunks i = (it WPS + rank) 64 + lane of K
+        // (to the bf16 K tile now) and of V (held until every wave has read its fp8 chunks, since
+        // the bf16 V tile overwrites them).
+        constexpr int CHUNKS = TILE * HD / 16;  // 16-byte fp8 chunks per tile
+        constexpr int IT = (CHUNKS + WAVE * WPS - 1) / (WAVE * WPS);
+        u32x4_t v8[IT];
+        // The slot arithmetic is redone each round from an opaque copy of the lane id: hoisted out
+        // of the round loop, its 12 addresses would be held in registers through the tile math.
+        int ln = rank * WAVE + lane;
+        asm volatile("" : "+v"(ln));
+        if (has) {
+#pragma unroll
+          for (int it = 0; it < IT; ++it) {
+            const int i = it * WPS * WAVE + ln, r = i >> 4, q = i & 15;
+            if (i < CHUNKS) {  // uniform per wave
+              v8[it] = vt[CHUNKS + i];
+              const u32x4_t k8 = vt[i];
+              kt[tile::k_slot(r, 2 * q)] = fp8x8_to_bf16x8(u32x2_t{k8[0], k8[1]});
+              kt[tile::k_slot(r, 2 * q + 1)] = fp8x8_to_bf16x8(u32x2_t{k8[2], k8[3]});
+            }
+          }
+        }
+        __syncthreads();  // the bf16 K tile is whole, and no fp8 chunk is read again
+        if (has) {
+#pragma unroll
+          for (int it = 0; it < IT; ++it) {
+            const int i = it * WPS * WAVE + ln, r = i >> 4, q = i & 15;
+            if (i < CHUNKS) {
+              vt[r * ROW_CHUNKS + ((2 * q) ^ tile::v_swz(r))] =
+                  fp8x8_to_bf16x8(u32x2_t{v8[it][0], v8[it][1]});
+              vt[r * ROW_CHUNKS + ((2 * q + 1) ^ tile::v_swz(r))] =
+                  fp8x8_to_bf16x8(u32x2_t{v8[it][2], v8[it][3]});
+            }
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the K operand reads below the conversion
+      }
+      f32x4_t sacc[CPW][2];
+      u32x4_t pb_hi[CPW], pb_lo[CPW];
       if (has) {
-        f32x4_t sacc[CPW][2];
-        if constexpr (KV8) qk_tile8<CPW>(kt, qb, c, g4, sacc);
-        else tile::qk_tile<CPW>(kt, qb, c, g4, sacc);
-        u32x4_t pb_hi[CPW], pb_lo[CPW];
+        tile::qk_tile<CPW>(kt, qb, c, g4, sacc);
         if (p0 + TILE > P.Lmin)
           tile::softmax_tile<CPW, true, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
         else
           tile::softmax_tile<CPW, false, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
-        if constexpr (KV8) {
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            u32x4_t vr[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const int row = 16 * (e >> 2) + 4 * g4 + (e & 3);
-              vr[e] = fp8x8_to_bf16x8(*reinterpret_cast<const u32x2_t*>(
-                  reinterpret_cast<const char*>(vt) + row * HD + 128 * hh + 8 * c));
-            }
-            tile::pv_half<CPW, true>(vr, hh, pb_hi, pb_lo, acc);
-          }
-        } else {
-          tile::pv_tile_tr<CPW, true>(vt, lane, g4, pb_hi, pb_lo, acc);
-        }
       }
+      if constexpr (KV8) __syncthreads();  // the bf16 V tile is whole
+      if (has) tile::pv_tile_tr<CPW, true>(vt, lane, g4, pb_hi, pb_lo, acc);
       __syncthreads();  // this round's tiles are read before the next round overwrites them
     }
 
@@ -887,19 +910,10 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
           }
           const int t = col / grp, head = g * grp + (col - t * grp);
           float* dst = part_o + (((size_t)t * Hq + head) * NS + s) * HD;
-          if constexpr (KV8) {
-            // acc[8hh + i][ii] = O^T[128hh + 32g4 + 8ii + i] (tile::pv_half)
-            const int h = sub >> 1, i0 = 4 * (sub & 1);
+          // acc[i][k] = O^T[16i + 4g4 + k] (tile::pv_tile_tr)
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii)
-              reinterpret_cast<f32x4_t*>(dst + 128 * h + 32 * g4 + i0 + 8 * ii)[0] =
-                  f32x4_t{mo[0][ii], mo[1][ii], mo[2][ii], mo[3][ii]};
-          } else {
-            // acc[i][k] = O^T[16i + 4g4 + k] (tile::pv_tile_tr)
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-              reinterpret_cast<f32x4_t*>(dst + 16 * (4 * sub + k) + 4 * g4)[0] = mo[k];
-          }
+          for (int k = 0; k < 4; ++k)
+            reinterpret_cast<f32x4_t*>(dst + 16 * (4 * sub + k) + 4 * g4)[0] = mo[k];
         }
         __syncthreads();  // (also ends the pass: the next pass's loads may overwrite `lds`)
       }
