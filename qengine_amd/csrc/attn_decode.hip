@@ -698,11 +698,12 @@ constexpr int REGION_U4 = 2 * TILE_U4;       // a subset's K tile then V tile
 }  // namespace cols
 
 // KV8: an fp8 cache (E4M3FN codes). The subset's 8 KB fp8 K and V tiles land row-major in its
-// 16 KB bf16 V region (K, then V); its waves convert them once (exactly: every E4M3 value is a
-// bf16 value) into the bf16 K and V tiles, laid out and swizzled as the bf16 path loads them, and
-// the tile arithmetic below runs unchanged. So with scales of 1 the result equals the bf16
-// kernel's on the dequantized cache, bit for bit. Converting once instead of in every wave that
-// reads a tile took the 8-row verify from 17.1 to 14.6 us (partials, 4k) and 29.0 to 25.2 (16k).
+// 16 KB bf16 V region (K, then V). All waves of the workgroup then convert the round's tiles once
+// (exactly: every E4M3 value is a bf16 value) into the bf16 K and V tiles, laid out and swizzled as
+// the bf16 path loads them, and the tile arithmetic below runs unchanged. So with scales of 1 the
+// result equals the bf16 kernel's on the dequantized cache, bit for bit. Converting once instead
+// of in every wave that reads a tile took the 8-row verify from 17.1 to 14.7 us (partials, 4k)
+// and 29.0 to 25.0 (16k).
 template <int NT, int CPW, bool KV8 = false>
 __global__ void __launch_bounds__(cols::SUBSETS * (NT / CPW) * WAVE)
 attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
@@ -804,39 +805,40 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
       vmcnt_wait<0>();
       __syncthreads();  // every wave's loads of this round have landed
       if constexpr (KV8) {
-        // Convert once: thread (rank, lane) takes fp8 chunks i = (it WPS + rank) 64 + lane of K
-        // (to the bf16 K tile now) and of V (held until every wave has read its fp8 chunks, since
-        // the bf16 V tile overwrites them).
+        // Convert once, all waves of the workgroup together: chunk gk of the active subsets'
+        // tiles (subset gk / 512, chunk gk % 512) goes to thread gk % (64 SUB WPS).
         constexpr int CHUNKS = TILE * HD / 16;  // 16-byte fp8 chunks per tile
-        constexpr int IT = (CHUNKS + WAVE * WPS - 1) / (WAVE * WPS);
+        constexpr int NTH = SUB * WPS * WAVE;
+        constexpr int IT = (SUB * CHUNKS + NTH - 1) / NTH;
+        const int rem = P.end - (P.beg + r * SUB * TILE);
+        const int nact = min(SUB, (rem + TILE - 1) / TILE);  // active subsets this round (>= 1)
         u32x4_t v8[IT];
-        // The slot arithmetic is redone each round from an opaque copy of the lane id: hoisted out
-        // of the round loop, its 12 addresses would be held in registers through the tile math.
-        int ln = rank * WAVE + lane;
-        asm volatile("" : "+v"(ln));
-        if (has) {
+        int tid = threadIdx.x;  // opaque: the slot arithmetic is redone each round
+        asm volatile("" : "+v"(tid));
 #pragma unroll
-          for (int it = 0; it < IT; ++it) {
-            const int i = it * WPS * WAVE + ln, r = i >> 4, q = i & 15;
-            if (i < CHUNKS) {  // uniform per wave
-              v8[it] = vt[CHUNKS + i];
-              const u32x4_t k8 = vt[i];
-              kt[tile::k_slot(r, 2 * q)] = fp8x8_to_bf16x8(u32x2_t{k8[0], k8[1]});
-              kt[tile::k_slot(r, 2 * q + 1)] = fp8x8_to_bf16x8(u32x2_t{k8[2], k8[3]});
-            }
+        for (int it = 0; it < IT; ++it) {
+          const int gk = it * NTH + tid;
+          if (gk < nact * CHUNKS) {  // uniform per wave
+            const int ss = gk / CHUNKS, i = gk % CHUNKS, rr = i >> 4, q = i & 15;
+            u32x4_t* kts = lds + ss * cols::REGION_U4;
+            const u32x4_t* vts = kts + cols::TILE_U4;
+            v8[it] = vts[CHUNKS + i];
+            const u32x4_t k8 = vts[i];
+            kts[tile::k_slot(rr, 2 * q)] = fp8x8_to_bf16x8(u32x2_t{k8[0], k8[1]});
+            kts[tile::k_slot(rr, 2 * q + 1)] = fp8x8_to_bf16x8(u32x2_t{k8[2], k8[3]});
           }
         }
-        __syncthreads();  // the bf16 K tile is whole, and no fp8 chunk is read again
-        if (has) {
+        __syncthreads();  // the bf16 K tiles are whole, and no fp8 chunk is read again
 #pragma unroll
-          for (int it = 0; it < IT; ++it) {
-            const int i = it * WPS * WAVE + ln, r = i >> 4, q = i & 15;
-            if (i < CHUNKS) {
-              vt[r * ROW_CHUNKS + ((2 * q) ^ tile::v_swz(r))] =
-                  fp8x8_to_bf16x8(u32x2_t{v8[it][0], v8[it][1]});
-              vt[r * ROW_CHUNKS + ((2 * q + 1) ^ tile::v_swz(r))] =
-                  fp8x8_to_bf16x8(u32x2_t{v8[it][2], v8[it][3]});
-            }
+        for (int it = 0; it < IT; ++it) {
+          const int gk = it * NTH + tid;
+          if (gk < nact * CHUNKS) {
+            const int ss = gk / CHUNKS, i = gk % CHUNKS, rr = i >> 4, q = i & 15;
+            u32x4_t* vts = lds + ss * cols::REGION_U4 + cols::TILE_U4;
+            vts[rr * ROW_CHUNKS + ((2 * q) ^ tile::v_swz(rr))] =
+                fp8x8_to_bf16x8(u32x2_t{v8[it][0], v8[it][1]});
+            vts[rr * ROW_CHUNKS + ((2 * q + 1) ^ tile::v_swz(rr))] =
+                fp8x8_to_bf16x8(u32x2_t{v8[it][2], v8[it][3]});
           }
         }
         __builtin_amdgcn_sched_barrier(0);  // keep the K operand reads below the conversion
