@@ -27,16 +27,30 @@ constexpr float LAZY_TAU = 8.f;          // log2 headroom before the reference m
 __device__ __forceinline__ int k_slot(int r, int q) { return r * ROW_CHUNKS + (q ^ (r & 15)); }
 
 // S^T for one tile: sacc[ct][T] holds positions p0 + 16T + 4g4 + i of column ct*16 + c.
+// Lane (c, g4) reads chunk 4ks + g4 of row 16T + c, at slot k_slot(16T + c, 4ks + g4). Since
+// (4ks + g4) ^ c = 4 (ks ^ (c >> 2)) + (g4 ^ (c & 3)) and ks ^ (c >> 2) = 4 (ks >> 2) +
+// ((ks & 3) ^ (c >> 2)), the byte offset is kl[ks & 3] + 256 (ks >> 2) + 8192 T with four
+// per-lane bases: one address add per base and tile, the rest immediate offsets (about 25 fewer
+// VALU instructions per tile). Callers with two or more column tiles per wave sit at the register
+// limit and keep the per-read slot arithmetic, which needs no extra live registers.
 template <int NT>
 __device__ __forceinline__ void qk_tile(const u32x4_t* k_lds, const bf16x8_t (&qb)[NT][8], int c,
                                         int g4, f32x4_t (&sacc)[NT][2]) {
+  const char* kb = reinterpret_cast<const char*>(k_lds);
+  const char* kl[4];
+#pragma unroll
+  for (int l = 0; l < 4; ++l)
+    kl[l] = kb + c * (ROW_CHUNKS * 16) + 64 * (l ^ (c >> 2)) + 16 * (g4 ^ (c & 3));
 #pragma unroll
   for (int T = 0; T < 2; ++T) {
 #pragma unroll
     for (int ct = 0; ct < NT; ++ct) sacc[ct][T] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-      const bf16x8_t kop = as_bf16x8(k_lds[k_slot(16 * T + c, 4 * ks + g4)]);
+      const bf16x8_t kop =
+          NT == 1 ? as_bf16x8(*reinterpret_cast<const u32x4_t*>(kl[ks & 3] + 256 * (ks >> 2) +
+                                                                 16 * ROW_CHUNKS * 16 * T))
+                  : as_bf16x8(k_lds[k_slot(16 * T + c, 4 * ks + g4)]);
 #pragma unroll
       for (int ct = 0; ct < NT; ++ct) sacc[ct][T] = mfma16x16x32(kop, qb[ct][ks], sacc[ct][T]);
     }
@@ -144,10 +158,18 @@ __device__ __forceinline__ void pv_tile_tr(const u32x4_t* vt, int lane, int g4,
   typedef short v4i16 __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
   const int a = lane & 3, r = 4 * g4 + ((lane >> 2) & 3);
-  char* vb = const_cast<char*>(reinterpret_cast<const char*>(vt)) + r * (HD * 2) + (a & 1) * 8;
+  // Chunk (2i + (a >> 1)) ^ v_swz(r) = 2 (i ^ (r & 7)) + (a >> 1) = 16 (i >> 3) + 2 ((i & 7) ^
+  // (r & 7)) + (a >> 1): eight per-lane bases vl[i & 7], and 256 (i >> 3) as an immediate offset.
+  // (The bases cost registers: callers with two or more column tiles per wave compute each
+  // address from the swizzle instead.)
+  char* vr = const_cast<char*>(reinterpret_cast<const char*>(vt)) + r * (HD * 2) + (a & 1) * 8;
+  char* vl[8];
+#pragma unroll
+  for (int l = 0; l < 8; ++l) vl[l] = vr + 16 * (a >> 1) + 32 * (l ^ (r & 7));
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    char* p = vb + ((2 * i + (a >> 1)) ^ v_swz(r)) * 16;  // rows r and r + 16 share the swizzle
+    char* p = NT == 1 ? vl[i & 7] + 256 * (i >> 3)  // rows r and r + 16 share the swizzle
+                      : vr + ((2 * i + (a >> 1)) ^ v_swz(r)) * 16;
     const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
         reinterpret_cast<lds_v4i16*>((__attribute__((address_space(3))) char*)p));
     const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(

@@ -23,11 +23,12 @@ __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to
 __device__ __forceinline__ float lo_bf16(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float hi_bf16(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 
-// Pack two fp32 into a dword of two bf16 (round to nearest even): a -> low half, b -> high.
+// Pack two fp32 into a dword of two bf16 (round to nearest even): a -> low half, b -> high. One
+// v_cvt_pk_bf16_f32 on gfx950 (two scalar conversions would need a shift and an or on top).
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  const uint32_t lo = __builtin_bit_cast(uint16_t, f32_to_bf16(a));
-  const uint32_t hi = __builtin_bit_cast(uint16_t, f32_to_bf16(b));
-  return lo | (hi << 16);
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
 
 // dword made of the low halves (sel_hi = false) or high halves (true) of x (-> low) and y (-> high)
