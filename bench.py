@@ -543,7 +543,7 @@ def gdn_alg_bytes(n: int, pend: int, hk: int = GDN_HK, hv: int = GDN_HV) -> int:
     return state + staged + conv + rows + hv * 2 * 2 + 128 * 2
 
 
-def bench_gdn(torch, C, steps: int, warmup: int) -> dict:
+def bench_gdn(torch, C, steps: int, warmup: int, rows=(1, 2, 4, 6, 8)) -> dict:
     """Gated DeltaNet step (gdn_step_n) at the reference model's shapes (Hk 16, Hv 48: 48 value
     heads with a 128 x 128 fp32 state, 3 MB per layer), the way the reference times it
     (bench/engine/micro_kernels.py:35-56): 48 layer-calls per graph on separate states, with
@@ -573,7 +573,7 @@ def bench_gdn(torch, C, steps: int, warmup: int) -> dict:
                      *Ld["st"], ctl, out[:n], hk, 1e-6)
 
     res = {}
-    for n in (1, 2, 4, 6, 8):
+    for n in rows:
         sets = [[layer() for _ in range(nl)] for _ in range(2)]
         prime = torch.tensor([100, 0, 0, 0, 0, 0, 0, 0], dtype=I32, device=dev)
         ctl = torch.tensor([100, n, 0, 0, 0, 0, 0, 0], dtype=I32, device=dev)
@@ -746,6 +746,8 @@ def main():
                     help="only embed / rmsnorm1p / swiglu / argmax / accept+commit, as JSON")
     ap.add_argument("--gdn-only", action="store_true",
                     help="only the Gated DeltaNet step at the model's shapes, as JSON")
+    ap.add_argument("--gdn-rows", default="1,2,4,6,8",
+                    help="row counts of the --gdn-only leg (one profile per row count)")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the in_proj / o_proj GEMV and the HBM read probe, as JSON")
     ap.add_argument("--sweep-only", action="store_true",
@@ -794,7 +796,8 @@ def main():
         print(json.dumps(bench_step_ops(torch, C, args.steps, args.warmup)))
         return
     if args.gdn_only:
-        print(json.dumps(bench_gdn(torch, C, args.steps, args.warmup)))
+        rows = tuple(int(x) for x in args.gdn_rows.split(",") if x)
+        print(json.dumps(bench_gdn(torch, C, args.steps, args.warmup, rows)))
         return
     lengths = [int(x) for x in args.lengths.split(",") if x]
     if args.sweep_only:
