@@ -31,6 +31,9 @@ def run_prefill(C, q, kc, vc, pos, qg):
     (24, 4, 128, 1000, 1100),  # cache longer than the chunk needs
     (4, 4, 64, 0, 64),         # no GQA
     (24, 4, 200, 100, 250),    # rows past the end of the cache attend the whole cache
+    (12, 2, 16, 0, 16),        # GQA 6, one 16-row block (the balanced layout's half pair)
+    (24, 4, 17, 3, 30),        # GQA 6, two blocks, the second ragged
+    (6, 1, 48, 700, 760),      # GQA 6, one KV head, three blocks
 ])
 def test_prefill_matches_oracle(native, hq, hkv, T, pos, max_len):
     g = gen(hq * 1000 + T)
@@ -43,9 +46,10 @@ def test_prefill_matches_oracle(native, hq, hkv, T, pos, max_len):
     assert ok, (mx, mean)
 
 
-def test_prefill_ignores_unattended_cache(native):
-    hq, hkv, T, pos, max_len = 8, 2, 96, 40, 400
-    g = gen(77)
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (24, 4)])  # the 8-wave and the balanced layout
+def test_prefill_ignores_unattended_cache(native, hq, hkv):
+    T, pos, max_len = 96, 40, 400
+    g = gen(77 + hq)
     kc = torch.randn(hkv, max_len, D, generator=g).to(BF)
     vc = torch.randn(hkv, max_len, D, generator=g).to(BF)
     q = torch.randn(T, hq * D, generator=g).to(BF)
