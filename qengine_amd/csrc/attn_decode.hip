@@ -697,6 +697,49 @@ constexpr int TILE_U4 = TILE * ROW_CHUNKS;   // 16-byte slots of one K (or V) ti
 constexpr int REGION_U4 = 2 * TILE_U4;       // a subset's K tile then V tile
 }  // namespace cols
 
+// bf16 rounds of attn_partials_cols_kernel with split K/V look-ahead: round 0's K and V tiles
+// load together; after that the V tile of round r loads while the subset computes S^T and the
+// softmax of round r, and the K tile of round r+1 while it computes O^T += V^T P^T. Each half takes its LDS operands and the LDS-DMA target as
+// distinct __restrict__ pointers, so the compiler's wait-count pass sees that the operand reads
+// do not depend on the DMA just issued (without that it waits for it before the first read).
+namespace cols {
+// 16 one-KB LDS-DMA loads of a K (or V) tile, rows 2i, 2i+1, shared by the subset's WPS waves
+template <bool IS_V>
+__device__ __forceinline__ void issue_kv(__amdgpu_buffer_rsrc_t rs, int p0, u32x4_t* dst, int rank,
+                                         int wps, int lane) {
+  for (int i = rank; i < 16; i += wps) {
+    const int row = 2 * i + (lane >> 5);
+    const int q = IS_V ? (lane & 31) ^ tile::v_swz(row) : (lane & 31) ^ (row & 15);
+    buffer_load16_to_lds(rs, (uint32_t)(p0 + row) * (HD * 2) + q * 16, dst + 2 * i * ROW_CHUNKS);
+  }
+}
+template <int CPW>
+__device__ __forceinline__ void qk_softmax_half(
+    const u32x4_t* __restrict__ kt, u32x4_t* __restrict__ v_dst, bool has, bool load_v, int p0,
+    int Lmin, __amdgpu_buffer_rsrc_t vrs, int rank, int wps, int lane, int c, int g4,
+    const bf16x8_t (&qb)[CPW][8], const int (&Lcol)[CPW], float scale_log2, float (&m)[CPW],
+    float (&l)[CPW], f32x4_t (&acc)[CPW][16], u32x4_t (&pb_hi)[CPW], u32x4_t (&pb_lo)[CPW]) {
+  if (load_v) issue_kv<true>(vrs, p0, v_dst, rank, wps, lane);
+  if (!has) return;
+  f32x4_t sacc[CPW][2];
+  tile::qk_tile<CPW>(kt, qb, c, g4, sacc);
+  if (p0 + TILE > Lmin)
+    tile::softmax_tile<CPW, true, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
+  else
+    tile::softmax_tile<CPW, false, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
+}
+template <int CPW>
+__device__ __forceinline__ void pv_half_la(const u32x4_t* __restrict__ vt,
+                                           u32x4_t* __restrict__ k_dst, bool has, bool load_k,
+                                           int p0_next, __amdgpu_buffer_rsrc_t krs, int rank,
+                                           int wps, int lane, int g4,
+                                           const u32x4_t (&pb_hi)[CPW], const u32x4_t (&pb_lo)[CPW],
+                                           f32x4_t (&acc)[CPW][16]) {
+  if (load_k) issue_kv<false>(krs, p0_next, k_dst, rank, wps, lane);
+  if (has) tile::pv_tile_tr<CPW, true>(vt, lane, g4, pb_hi, pb_lo, acc);
+}
+}  // namespace cols
+
 // KV8: an fp8 cache (E4M3FN codes). The subset's 8 KB fp8 K and V tiles land row-major in its
 // 16 KB bf16 V region (K, then V). All waves of the workgroup then convert the round's tiles once
 // (exactly: every E4M3 value is a bf16 value) into the bf16 K and V tiles, laid out and swizzled as
@@ -778,6 +821,36 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
 
     const int ntiles = (P.end - P.beg + TILE - 1) / TILE;
     const int rounds = (ntiles + SUB - 1) / SUB;
+    if constexpr (!KV8 && CPW == 1) {
+      // Two barriers per round as before (one when the pass has one round); each one also
+      // publishes the tile loaded during the half-round before it. (CPW = 2 keeps the loop below:
+      // there the look-ahead's longer-lived addresses add spills, 30 -> 70, and it ran 17-42%
+      // slower at GQA 8.)
+      const int p00 = P.beg + sub * TILE;
+      if (p00 < P.end) {
+        cols::issue_kv<false>(krs, p00, kt, rank, WPS, lane);
+        cols::issue_kv<true>(vrs, p00, vt, rank, WPS, lane);
+      }
+      vmcnt_wait<0>();
+      __syncthreads();  // K and V of round 0 have landed
+      for (int r = 0; r < rounds; ++r) {
+        const int p0 = P.beg + (r * SUB + sub) * TILE;  // this subset's tile in round r
+        const bool has = p0 < P.end;                     // uniform per subset
+        const int p1 = p0 + SUB * TILE;
+        const bool has1 = r + 1 < rounds && p1 < P.end;
+        u32x4_t pb_hi[CPW], pb_lo[CPW];
+        cols::qk_softmax_half<CPW>(kt, vt, has, has && r > 0, p0, P.Lmin, vrs, rank, WPS, lane, c, g4, qb,
+                                   Lcol, scale_log2, m, l, acc, pb_hi, pb_lo);
+        // (The wait stays outside the branch: behind a join the compiler's wait-count pass
+        // assumes V may still be in flight and waits for the K load below before PV.)
+        vmcnt_wait<0>();
+        if (r > 0 || r + 1 < rounds)  // uniform
+          __syncthreads();  // V of round r has landed; K of round r is no longer read
+        cols::pv_half_la<CPW>(vt, kt, has, has1, p1, krs, rank, WPS, lane, g4, pb_hi, pb_lo, acc);
+        vmcnt_wait<0>();
+        __syncthreads();  // K of round r+1 has landed; V of round r is no longer read
+      }
+    } else
     for (int r = 0; r < rounds; ++r) {
       const int p0 = P.beg + (r * SUB + sub) * TILE;  // this subset's tile in round r
       const bool has = p0 < P.end;                     // uniform per subset

@@ -225,6 +225,26 @@ def test_rows_straddling_a_slice_size_change(native, hq, hkv, n, pos, ns):
         assert torch.equal(o1[0], out[t]), t
 
 
+@pytest.mark.parametrize("hq,hkv,n,pos,ns", [
+    (24, 4, 8, 3000, 8),    # slices of 384: 12 tiles, 3 rounds of the 4 position subsets
+    (24, 4, 6, 5000, 4),    # slices of 1280: 40 tiles, 10 rounds (the last slice: 37 tiles)
+    (24, 4, 7, 4090, 16),   # slices of 256 | 288: 2 and 3 rounds, one pass per size
+    (24, 4, 8, 700, 2),     # slices of 352 | 384: 11 tiles leave 3 of 4 subsets in round 3
+    (32, 8, 8, 3000, 8),    # four column tiles (two per wave)
+])
+def test_multi_round_slices(native, hq, hkv, n, pos, ns):
+    """6-8 rows (3-4 MFMA column tiles) over slices of several rounds of tiles, where each round's
+    K and V loads overlap the previous half-round's arithmetic: results match the oracle and each
+    row is bit-identical to a 1-row call."""
+    case = decode_case(seed=pos + ns, hq=hq, hkv=hkv, pos=pos, n=n, max_len=pos + n + 24)
+    out = gpu_decode(native, case, ns)
+    ok, mx, mean = attn_close(out, oracle_decode(case))
+    assert ok, (mx, mean)
+    for t in range(n):
+        o1 = gpu_decode(native, case, ns, pos=case.pos + t, rows=slice(t, t + 1))
+        assert torch.equal(o1[0], out[t]), t
+
+
 @pytest.mark.parametrize("n", [3, 5])
 def test_two_tile_kernels_give_the_same_bits(native, n):
     """3-5 rows (two MFMA column tiles) take the multi-column kernel when every slice of the cache
