@@ -697,13 +697,19 @@ constexpr int TILE_U4 = TILE * ROW_CHUNKS;   // 16-byte slots of one K (or V) ti
 constexpr int REGION_U4 = 2 * TILE_U4;       // a subset's K tile then V tile
 }  // namespace cols
 
-// bf16 rounds of attn_partials_cols_kernel with split K/V look-ahead: round 0's K and V tiles
-// load together; after that the V tile of round r loads while the subset computes S^T and the
-// softmax of round r, and the K tile of round r+1 while it computes O^T += V^T P^T. Each half takes its LDS operands and the LDS-DMA target as
-// distinct __restrict__ pointers, so the compiler's wait-count pass sees that the operand reads
-// do not depend on the DMA just issued (without that it waits for it before the first read).
+// Look-ahead rounds of attn_partials_cols_kernel (one column tile per wave). bf16 cache: round
+// 0's K and V tiles load together; after that the V tile of round r loads while the subset
+// computes S^T and the softmax of round r, and the K tile of round r+1 while it computes
+// O^T += V^T P^T. fp8 cache: the fp8 K tile of round r+1 loads into the subset's 8 KB staging
+// buffer during S^T and the softmax of round r, is converted into the bf16 K tile, and the fp8
+// V tile of round r+1 then loads into the same buffer during O^T += V^T P^T. Each half takes its
+// LDS operands and the LDS-DMA target as distinct __restrict__ pointers, so the compiler's
+// wait-count pass sees that the operand reads do not depend on the DMA just issued (without that
+// it waits for it before the first read).
 namespace cols {
-// 16 one-KB LDS-DMA loads of a K (or V) tile, rows 2i, 2i+1, shared by the subset's WPS waves
+constexpr int STAGE8_U4 = TILE * HD / 16;  // 16-byte slots of one fp8 tile: 8 KB
+
+// 16 one-KB LDS-DMA loads of a bf16 K (or V) tile, rows 2i, 2i+1, shared by the subset's waves
 template <bool IS_V>
 __device__ __forceinline__ void issue_kv(__amdgpu_buffer_rsrc_t rs, int p0, u32x4_t* dst, int rank,
                                          int wps, int lane) {
@@ -713,13 +719,30 @@ __device__ __forceinline__ void issue_kv(__amdgpu_buffer_rsrc_t rs, int p0, u32x
     buffer_load16_to_lds(rs, (uint32_t)(p0 + row) * (HD * 2) + q * 16, dst + 2 * i * ROW_CHUNKS);
   }
 }
-template <int CPW>
+// 8 one-KB LDS-DMA loads of an fp8 tile, rows 4i .. 4i+3, row-major (chunk q of row r at 16 r + q)
+__device__ __forceinline__ void issue_fp8(__amdgpu_buffer_rsrc_t rs, int p0, u32x4_t* dst, int rank,
+                                          int wps, int lane) {
+  for (int i = rank; i < 8; i += wps) {
+    const int row = 4 * i + (lane >> 4);
+    buffer_load16_to_lds(rs, (uint32_t)(p0 + row) * HD + (lane & 15) * 16, dst + 64 * i);
+  }
+}
+// LD: what the half loads (0 a bf16 V tile, 1 a bf16 K tile, 2 an fp8 tile)
+template <int LD>
+__device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, int p, u32x4_t* dst, int rank,
+                                      int wps, int lane) {
+  if constexpr (LD == 2)
+    issue_fp8(rs, p, dst, rank, wps, lane);
+  else
+    issue_kv<LD == 0>(rs, p, dst, rank, wps, lane);
+}
+template <int CPW, int LD>
 __device__ __forceinline__ void qk_softmax_half(
-    const u32x4_t* __restrict__ kt, u32x4_t* __restrict__ v_dst, bool has, bool load_v, int p0,
-    int Lmin, __amdgpu_buffer_rsrc_t vrs, int rank, int wps, int lane, int c, int g4,
+    const u32x4_t* __restrict__ kt, u32x4_t* __restrict__ dst, bool has, bool load, int p_load,
+    __amdgpu_buffer_rsrc_t rs, int p0, int Lmin, int rank, int wps, int lane, int c, int g4,
     const bf16x8_t (&qb)[CPW][8], const int (&Lcol)[CPW], float scale_log2, float (&m)[CPW],
     float (&l)[CPW], f32x4_t (&acc)[CPW][16], u32x4_t (&pb_hi)[CPW], u32x4_t (&pb_lo)[CPW]) {
-  if (load_v) issue_kv<true>(vrs, p0, v_dst, rank, wps, lane);
+  if (load) issue<LD>(rs, p_load, dst, rank, wps, lane);
   if (!has) return;
   f32x4_t sacc[CPW][2];
   tile::qk_tile<CPW>(kt, qb, c, g4, sacc);
@@ -728,25 +751,55 @@ __device__ __forceinline__ void qk_softmax_half(
   else
     tile::softmax_tile<CPW, false, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
 }
-template <int CPW>
+template <int CPW, int LD>
 __device__ __forceinline__ void pv_half_la(const u32x4_t* __restrict__ vt,
-                                           u32x4_t* __restrict__ k_dst, bool has, bool load_k,
-                                           int p0_next, __amdgpu_buffer_rsrc_t krs, int rank,
+                                           u32x4_t* __restrict__ dst, bool has, bool load,
+                                           int p_load, __amdgpu_buffer_rsrc_t rs, int rank,
                                            int wps, int lane, int g4,
                                            const u32x4_t (&pb_hi)[CPW], const u32x4_t (&pb_lo)[CPW],
                                            f32x4_t (&acc)[CPW][16]) {
-  if (load_k) issue_kv<false>(krs, p0_next, k_dst, rank, wps, lane);
+  if (load) issue<LD>(rs, p_load, dst, rank, wps, lane);
   if (has) tile::pv_tile_tr<CPW, true>(vt, lane, g4, pb_hi, pb_lo, acc);
+}
+// All NTH threads of the workgroup convert the fp8 tiles of the first nact subsets once, from
+// `src` (row-major) to `dst` (the bf16 K or V tile layout) in each subset's region of `region`
+// slots. Every E4M3 value is a bf16 value, so the conversion is exact.
+template <bool IS_V, int NTH>
+__device__ __forceinline__ void convert_fp8(u32x4_t* lds, int region, int src_off, int dst_off,
+                                            int nact) {
+  constexpr int IT = (SUBSETS * STAGE8_U4 + NTH - 1) / NTH;
+  int tid = threadIdx.x;  // opaque: the slot arithmetic is redone at each call
+  asm volatile("" : "+v"(tid));
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int gk = it * NTH + tid;
+    if (gk < nact * STAGE8_U4) {  // uniform per wave
+      const int ss = gk / STAGE8_U4, i = gk % STAGE8_U4, rr = i >> 4, q = i & 15;
+      u32x4_t* base = lds + ss * region;
+      const u32x4_t c8 = base[src_off + i];
+      const u32x4_t lo = fp8x8_to_bf16x8(u32x2_t{c8[0], c8[1]});
+      const u32x4_t hi = fp8x8_to_bf16x8(u32x2_t{c8[2], c8[3]});
+      if constexpr (IS_V) {
+        base[dst_off + rr * ROW_CHUNKS + ((2 * q) ^ tile::v_swz(rr))] = lo;
+        base[dst_off + rr * ROW_CHUNKS + ((2 * q + 1) ^ tile::v_swz(rr))] = hi;
+      } else {
+        base[dst_off + tile::k_slot(rr, 2 * q)] = lo;
+        base[dst_off + tile::k_slot(rr, 2 * q + 1)] = hi;
+      }
+    }
+  }
 }
 }  // namespace cols
 
-// KV8: an fp8 cache (E4M3FN codes). The subset's 8 KB fp8 K and V tiles land row-major in its
-// 16 KB bf16 V region (K, then V). All waves of the workgroup then convert the round's tiles once
-// (exactly: every E4M3 value is a bf16 value) into the bf16 K and V tiles, laid out and swizzled as
-// the bf16 path loads them, and the tile arithmetic below runs unchanged. So with scales of 1 the
-// result equals the bf16 kernel's on the dequantized cache, bit for bit. Converting once instead
-// of in every wave that reads a tile took the 8-row verify from 17.1 to 14.7 us (partials, 4k)
-// and 29.0 to 25.0 (16k).
+// KV8: an fp8 cache (E4M3FN codes). The subset's 8 KB fp8 K and V tiles land row-major in LDS
+// and all waves of the workgroup convert each tile once (exactly: every E4M3 value is a bf16
+// value) into the bf16 K and V tiles, laid out and swizzled as the bf16 path loads them, so the
+// tile arithmetic runs unchanged. With scales of 1 the result equals the bf16 kernel's on the
+// dequantized cache, bit for bit. Converting once instead of in every wave that reads a tile took
+// the 8-row verify from 17.1 to 14.7 us (partials, 4k) and 29.0 to 25.0 (16k); the look-ahead
+// rounds (one column tile per wave: a staging buffer per subset, 160 KB of LDS) then took it to
+// 13.7 (4k), 21.6 (16k) and 30.2 (32k). With two column tiles per wave the fp8 tiles of a round
+// land in the subset's 16 KB V tile (K, then V) and are converted before its arithmetic.
 template <int NT, int CPW, bool KV8 = false>
 __global__ void __launch_bounds__(cols::SUBSETS * (NT / CPW) * WAVE)
 attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
@@ -788,12 +841,24 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
   const bool attendA = PA.beg < PA.end;
   if (!attendA && !(npass > 1 && PB.beg < PB.end)) return;  // uniform per workgroup
 
-  __shared__ __attribute__((aligned(16))) u32x4_t lds[SUB * cols::REGION_U4];  // 128 KB
-  __shared__ float s_m[SUB][16 * NT], s_l[SUB][16 * NT];
+  // fp8 with one column tile per wave: each subset's region also holds an 8 KB fp8 staging
+  // buffer (4 x 40 KB: all 160 KB of LDS), and s_m / s_l live in the ring past the merge's
+  // accumulators (the ring is idle once the rounds end).
+  constexpr bool LA8 = KV8 && CPW == 1;
+  constexpr int REGION = LA8 ? cols::REGION_U4 + cols::STAGE8_U4 : cols::REGION_U4;
+  __shared__ __attribute__((aligned(16))) u32x4_t lds[SUB * REGION];  // 128 KB or 160 KB
+  __shared__ float s_m_[LA8 ? 1 : SUB][16 * NT], s_l_[LA8 ? 1 : SUB][16 * NT];
+  static_assert(!LA8 || SUB * 16 * WAVE * 16 + 2 * SUB * 16 * NT * 4 <= SUB * REGION * 16,
+                "s_m and s_l fit the ring past the merge buffer");
+  float (*s_m)[16 * NT] =
+      LA8 ? reinterpret_cast<float (*)[16 * NT]>(lds + SUB * 16 * WAVE) : s_m_;
+  float (*s_l)[16 * NT] =
+      LA8 ? reinterpret_cast<float (*)[16 * NT]>(lds + SUB * 16 * WAVE) + SUB : s_l_;
   constexpr int ELEM = KV8 ? 1 : 2;  // bytes per cache value
   const size_t head_off = (size_t)g * max_len * HD * ELEM;  // bytes
-  u32x4_t* kt = lds + sub * cols::REGION_U4;
+  u32x4_t* kt = lds + sub * REGION;
   u32x4_t* vt = kt + cols::TILE_U4;
+  u32x4_t* st = vt + cols::TILE_U4;  // LA8: the fp8 staging buffer
 
   // One pass, inlined once per call of the lambda (a loop over passes would keep the merge's
   // loop-invariant addresses live through the tile rounds and spill).
@@ -839,16 +904,61 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
         const int p1 = p0 + SUB * TILE;
         const bool has1 = r + 1 < rounds && p1 < P.end;
         u32x4_t pb_hi[CPW], pb_lo[CPW];
-        cols::qk_softmax_half<CPW>(kt, vt, has, has && r > 0, p0, P.Lmin, vrs, rank, WPS, lane, c, g4, qb,
-                                   Lcol, scale_log2, m, l, acc, pb_hi, pb_lo);
+        cols::qk_softmax_half<CPW, 0>(kt, vt, has, has && r > 0, p0, vrs, p0, P.Lmin, rank, WPS,
+                                      lane, c, g4, qb, Lcol, scale_log2, m, l, acc, pb_hi, pb_lo);
         // (The wait stays outside the branch: behind a join the compiler's wait-count pass
         // assumes V may still be in flight and waits for the K load below before PV.)
         vmcnt_wait<0>();
         if (r > 0 || r + 1 < rounds)  // uniform
           __syncthreads();  // V of round r has landed; K of round r is no longer read
-        cols::pv_half_la<CPW>(vt, kt, has, has1, p1, krs, rank, WPS, lane, g4, pb_hi, pb_lo, acc);
+        cols::pv_half_la<CPW, 1>(vt, kt, has, has1, p1, krs, rank, WPS, lane, g4, pb_hi, pb_lo,
+                                 acc);
         vmcnt_wait<0>();
         __syncthreads();  // K of round r+1 has landed; V of round r is no longer read
+      }
+    } else if constexpr (LA8) {
+      constexpr int NTH = SUB * WPS * WAVE;
+      const auto nact = [&](int r) {  // active subsets of round r (>= 1 for r < rounds)
+        return min(SUB, (P.end - (P.beg + r * SUB * TILE) + TILE - 1) / TILE);
+      };
+      // Round 0: fp8 K into the staging buffer and fp8 V into the upper half of the bf16 K tile,
+      // together; V is converted first, then K over the slots V came from.
+      const int p00 = P.beg + sub * TILE;
+      if (p00 < P.end) {
+        cols::issue_fp8(krs, p00, st, rank, WPS, lane);
+        cols::issue_fp8(vrs, p00, kt + cols::STAGE8_U4, rank, WPS, lane);
+      }
+      vmcnt_wait<0>();
+      __syncthreads();  // the fp8 tiles of round 0 have landed
+      cols::convert_fp8<true, NTH>(lds, REGION, cols::STAGE8_U4, cols::TILE_U4, nact(0));
+      __syncthreads();  // bf16 V whole; its fp8 source is no longer read
+      cols::convert_fp8<false, NTH>(lds, REGION, 2 * cols::TILE_U4, 0, nact(0));
+      __syncthreads();  // bf16 K whole; the staging buffer is free
+      for (int r = 0; r < rounds; ++r) {
+        const int p0 = P.beg + (r * SUB + sub) * TILE;  // this subset's tile in round r
+        const bool has = p0 < P.end;                     // uniform per subset
+        const int p1 = p0 + SUB * TILE;
+        const bool more = r + 1 < rounds;                // uniform
+        const bool has1 = more && p1 < P.end;
+        u32x4_t pb_hi[CPW], pb_lo[CPW];
+        cols::qk_softmax_half<CPW, 2>(kt, st, has, has1, p1, krs, p0, P.Lmin, rank, WPS, lane, c,
+                                      g4, qb, Lcol, scale_log2, m, l, acc, pb_hi, pb_lo);
+        // (The waits stay outside the branches: behind a join the compiler's wait-count pass
+        // would assume a load in flight and wait for the next one before the operand reads.)
+        vmcnt_wait<0>();
+        if (more) {
+          __syncthreads();  // fp8 K of round r+1 has landed; bf16 K of round r is no longer read
+          cols::convert_fp8<false, NTH>(lds, REGION, 2 * cols::TILE_U4, 0, nact(r + 1));
+          __syncthreads();  // bf16 K of round r+1 whole; the staging buffer is free
+        }
+        cols::pv_half_la<CPW, 2>(vt, st, has, has1, p1, vrs, rank, WPS, lane, g4, pb_hi, pb_lo,
+                                 acc);
+        vmcnt_wait<0>();
+        __syncthreads();  // fp8 V of round r+1 has landed; bf16 V of round r is no longer read
+        if (more) {
+          cols::convert_fp8<true, NTH>(lds, REGION, 2 * cols::TILE_U4, cols::TILE_U4, nact(r + 1));
+          __syncthreads();  // bf16 V of round r+1 whole; the staging buffer is free
+        }
       }
     } else
     for (int r = 0; r < rounds; ++r) {

@@ -122,10 +122,14 @@ def test_prep_fp8_writes_the_oracle_codes(native, ks, vs):
         assert int(cache8.view(torch.uint8)[:, : pos].count_nonzero()) == 0  # nothing else written
 
 
-# 6-8 rows at GQA 6 and 8 (36-64 columns) run the multi-column kernel's fp8 mode
+# 6-8 rows at GQA 6 and 8 (36-64 columns) run the multi-column kernel's fp8 mode; the cases
+# after the first five give slices of 3-10 rounds of tiles (partial last rounds, two passes),
+# where the next round's fp8 tiles load during the current round's arithmetic
 @pytest.mark.parametrize("hq,hkv,n,pos,max_len,ns", [
     (24, 4, 6, 4090, 4096, 64), (24, 4, 8, 1000, 1100, 64), (24, 4, 7, 16370, 16384, 64),
-    (32, 4, 8, 600, 640, 16), (24, 4, 6, 2045, 2100, 64)])
+    (32, 4, 8, 600, 640, 16), (24, 4, 6, 2045, 2100, 64),
+    (24, 4, 8, 3000, 3030, 8), (24, 4, 6, 5000, 5030, 4), (24, 4, 7, 4090, 4120, 16),
+    (24, 4, 8, 700, 730, 2), (32, 8, 8, 3000, 3030, 8)])
 def test_fp8_wide_verify_scale_one_equals_bf16(native, hq, hkv, n, pos, max_len, ns):
     case = decode_case(seed=pos + 7 * n, hq=hq, hkv=hkv, pos=pos, n=n, max_len=max_len)
     kc8, vc8 = quantize_cache(case.kc, 1.0), quantize_cache(case.vc, 1.0)
