@@ -1109,87 +1109,153 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
 }
 
 // Log-sum-exp merge of the slices holding row t's positions + fused sigmoid output gate.
-// One wave per (head h, row t, 64-dim chunk z). Lane group sg = lane/16 owns slices
-// s = sg (mod 4) and 4 dims per lane. The loads of a batch of COMBINE_BATCH slices are all
-// issued before any of them is used, so up to 4*COMBINE_BATCH slices cost one memory round trip.
-// The groups are added in a fixed order, so the result depends only on row t's partials and slice
-// count, never on the other rows of the call.
-constexpr int COMBINE_DIMS = 64;
-constexpr int COMBINE_BATCH = 16;
+// One wave per (head h, row t, DIMS-dim chunk z); lane = (slice group sg, 4 dims). The slices of
+// a batch of 64 fall into 8 slice groups (s = s0 + 8b + gid, b < 8); each group's 8 slices are
+// summed in order b = 0..7 and the 8 group sums by the tree ((g0+g4)+(g1+g5))+((g2+g6)+(g3+g7)).
+// DIMS = 32: 8 lane groups of 8 lanes, one group per lane, the whole tree across lanes. DIMS = 64:
+// 4 lane groups of 16 lanes, groups gid = sg and sg + 4 per lane (two chains), the first tree
+// level within the lane and the other two across lanes. Both add in the same order, so they give
+// the same bits, and the launcher picks by the wave count. The result depends only on row
+// t's partials and slice count, never on the other rows of the call.
+// All loads of a batch are issued before any is used, so up to 64 slices cost one memory round
+// trip. A lone wave pays ~4 cycles for every VALU instruction, so the work after the loads sets
+// the kernel's length (per-wave stamps on the box: ~1 us of ~3.9 us for an earlier form with 16
+// slices per lane and a branch per slice). Hence no branches (every slot is loaded, its index
+// clamped to NS - 1, and the slots that do not count are selected away: m = -inf, weight 0,
+// data 0; adding those +0 leaves L and O unchanged, as neither is ever -0), a tree for the batch
+// maximum, and 32-dim chunks (half the slices per lane) while the grid stays small.
+constexpr long COMBINE_W32_MAX = 768;  // 32-dim chunks up to 4 rows at GQA 6 (measured)
 
+template <int DIMS>
+struct CombineShape {
+  static constexpr int LANES = DIMS / 4;       // lanes per slice group (4 dims each)
+  static constexpr int LG = WAVE / LANES;      // lane groups: 8 or 4
+  static constexpr int CPL = 8 / LG;           // slice groups (chains) per lane: 1 or 2
+  static constexpr int B = 8;                  // slices per chain per batch
+};
+
+// The 8 group values of a lane's chains combined in the tree ((g0+g4)+(g1+g5))+((g2+g6)+(g3+g7)).
+// LG = 8 (one chain, group g = sg): lane ^ 32 is g ^ 4, lane ^ 8 (DPP within each 16-lane row)
+// is g ^ 1, lane ^ 16 is g ^ 2. LG = 4 (chains g = sg and sg + 4): the first level is the lane's
+// own pair, then lane ^ 16 is g ^ 1 and lane ^ 32 is g ^ 2. Every lane ends with the same bits
+// (a + b == b + a).
+template <int CPL>
+__device__ __forceinline__ float tree_sum(const float (&v)[CPL]) {
+  if constexpr (CPL == 2) {
+    return xor32_pair(xor16_pair(v[0] + v[1], true), true);
+  } else {
+    float x = xor32_pair(v[0], true);
+    x = x + dpp<0x128>(x);  // row_ror:8 = lane ^ 8 within 16
+    return xor16_pair(x, true);
+  }
+}
+template <int CPL>
+__device__ __forceinline__ float tree_max(float v) {
+  if constexpr (CPL == 1) v = fmaxf(v, dpp<0x128>(v));
+  return xor32_pair(xor16_pair(v, false), false);
+}
+
+template <int DIMS>
 __global__ void __launch_bounds__(WAVE)
 attn_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml,
                     const int* __restrict__ pos_ptr, const __bf16* __restrict__ qg, long ldp,
                     __bf16* __restrict__ out, long ldo, int Hq, int max_len, int NS,
                     NsDiv nd, float v_scale) {
+  using S = CombineShape<DIMS>;
+  constexpr int LG = S::LG, CPL = S::CPL, B = S::B;
   const int h = blockIdx.x, t = blockIdx.y, z = blockIdx.z;
-  const int lane = threadIdx.x, c16 = lane & 15, sg = lane >> 4;
+  const int lane = threadIdx.x, cd = lane % S::LANES, sg = lane / S::LANES;
   const size_t base = ((size_t)t * Hq + h) * NS;
   const float* ml = part_ml + base * 2;
-  const int dim = z * COMBINE_DIMS + 4 * c16;
+  const int dim = z * DIMS + 4 * cd;
   const __bf16* gp = qg + (size_t)t * ldp + (size_t)h * 2 * HD + HD + dim;
 
   // The first batch of slices is loaded before pos arrives (every slot below NS exists in the
   // caller's buffers); slots past row t's slice count S are discarded by selection, so stale
-  // contents never reach the sums.
-  f32x4_t po[COMBINE_BATCH];
-  float2 mls[COMBINE_BATCH];
-  auto load_batch = [&](int s0, int lim) {
+  // contents never reach the sums. Chain k of this lane is slice group sg + LG k.
+  f32x4_t po[CPL][B];
+  float2 mls[CPL][B];
+  auto load_batch = [&](int s0) {
 #pragma unroll
-    for (int b = 0; b < COMBINE_BATCH; ++b) {
-      const int s = s0 + 4 * b + sg;
-      if (s < lim) {
-        po[b] = *reinterpret_cast<const f32x4_t*>(part_o + (base + s) * HD + dim);
-        mls[b] = *reinterpret_cast<const float2*>(ml + 2 * s);
+    for (int b = 0; b < B; ++b)
+#pragma unroll
+      for (int k = 0; k < CPL; ++k) {
+        const int s = min(s0 + 8 * b + sg + LG * k, NS - 1);
+        po[k][b] = *reinterpret_cast<const f32x4_t*>(part_o + (base + s) * HD + dim);
+        mls[k][b] = *reinterpret_cast<const float2*>(ml + 2 * s);
       }
-    }
   };
-  load_batch(0, NS);
+  load_batch(0);
   float gate[4];  // qg rows carry no alignment guarantee beyond 2 bytes
 #pragma unroll
   for (int i = 0; i < 4; ++i) gate[i] = bf16_to_f32(gp[i]);
   const int L_t = min(pos_ptr[0] + t + 1, max_len);
   const int CH = split_size(L_t, nd);  // slice s holds positions iff s * CH < L_t (s < NS)
 
-  f32x4_t O = {0.f, 0.f, 0.f, 0.f};
-  float L = 0.f, M = -INFINITY;
-  for (int s0 = 0; s0 < NS && s0 * CH < L_t; s0 += 4 * COMBINE_BATCH) {
-    if (s0 > 0) load_batch(s0, NS);
-    bool valid[COMBINE_BATCH];
+  f32x4_t O[CPL];
+  float L[CPL], M = -INFINITY;
 #pragma unroll
-    for (int b = 0; b < COMBINE_BATCH; ++b) {
-      const int sl = s0 + 4 * b + sg;
-      valid[b] = sl < NS && sl * CH < L_t;
-    }
+  for (int k = 0; k < CPL; ++k) {
+    O[k] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    L[k] = 0.f;
+  }
+  for (int s0 = 0; s0 < NS && s0 * CH < L_t; s0 += 64) {
+    if (s0 > 0) load_batch(s0);
+    float mv[CPL][B];  // the slot's max, -inf unless the slot counts
+#pragma unroll
+    for (int k = 0; k < CPL; ++k)
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        const int sl = s0 + 8 * b + sg + LG * k;
+        mv[k][b] = sl < NS && sl * CH < L_t ? mls[k][b].x : -INFINITY;
+      }
     // running max over all slices seen so far (every lane group, so M is wave-uniform)
-    float bm = M;
+    constexpr int NV = CPL * B;
+    float tm[NV];
 #pragma unroll
-    for (int b = 0; b < COMBINE_BATCH; ++b) bm = valid[b] ? fmaxf(bm, mls[b].x) : bm;
-    bm = group4_max(bm);
+    for (int k = 0; k < CPL; ++k)
+#pragma unroll
+      for (int b = 0; b < B; ++b) tm[k * B + b] = mv[k][b];
+#pragma unroll
+    for (int w = NV / 2; w >= 1; w /= 2)
+#pragma unroll
+      for (int j = 0; j < w; ++j) tm[j] = fmaxf(tm[j], tm[j + w]);
+    const float bm = tree_max<CPL>(fmaxf(M, tm[0]));
     if (bm != M) {  // rescale what was accumulated under the old max (exact no-op otherwise)
       const float r = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - bm);
-      O *= r;
-      L *= r;
+#pragma unroll
+      for (int k = 0; k < CPL; ++k) {
+        O[k] *= r;
+        L[k] *= r;
+      }
       M = bm;
     }
 #pragma unroll
-    for (int b = 0; b < COMBINE_BATCH; ++b) {
-      if (valid[b] && mls[b].x != -INFINITY) {
-        const float f = __builtin_amdgcn_exp2f(mls[b].x - M);
-        L += mls[b].y * f;
-        O += po[b] * f;
-      }
-    }
-  }
-  L = group4_sum(L);
+    for (int b = 0; b < B; ++b)
 #pragma unroll
-  for (int i = 0; i < 4; ++i) O[i] = group4_sum(O[i]);
+      for (int k = 0; k < CPL; ++k) {
+        const bool use = mv[k][b] != -INFINITY;
+        const float f = use ? __builtin_amdgcn_exp2f(mv[k][b] - M) : 0.f;
+        const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+        L[k] += (use ? mls[k][b].y : 0.f) * f;
+        O[k] += (use ? po[k][b] : zero) * f;
+      }
+  }
+  const float Lt = tree_sum<CPL>(L);
+  f32x4_t Ot;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float oc[CPL];
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) oc[k] = O[k][i];
+    Ot[i] = tree_sum<CPL>(oc);
+  }
   if (sg == 0) {
     __bf16* op = out + (size_t)t * ldo + (size_t)h * HD + dim;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       // attention output is a bf16 tensor (v_scale: the fp8 cache's V scale, else exactly 1)
-      const float o = round_bf16((O[i] / L) * v_scale);
+      const float o = round_bf16((Ot[i] / Lt) * v_scale);
       op[i] = f32_to_bf16(o * round_bf16(sigmoid_f32(gate[i])));
     }
   }
@@ -1260,9 +1326,15 @@ static hipError_t launch_partials(const void* q, const void* kc, const void* vc,
 static hipError_t launch_combine(const float* part_o, const float* part_ml, const int* pos,
                                  const void* qg, long ldp, void* out, long ldo, int n, int Hq,
                                  int max_len, int NS, hipStream_t stream, float v_scale = 1.f) {
-  attn_combine_kernel<<<dim3(Hq, n, HD / COMBINE_DIMS), dim3(WAVE), 0, stream>>>(
-      part_o, part_ml, pos, static_cast<const __bf16*>(qg), ldp, static_cast<__bf16*>(out), ldo,
-      Hq, max_len, NS, ns_div(NS), v_scale);
+  // 32-dim chunks while the grid stays within COMBINE_W32_MAX waves, else 64 (same bits)
+  const auto* Qg = static_cast<const __bf16*>(qg);
+  auto* Out = static_cast<__bf16*>(out);
+  if ((long)Hq * n * (HD / 32) <= COMBINE_W32_MAX)
+    attn_combine_kernel<32><<<dim3(Hq, n, HD / 32), dim3(WAVE), 0, stream>>>(
+        part_o, part_ml, pos, Qg, ldp, Out, ldo, Hq, max_len, NS, ns_div(NS), v_scale);
+  else
+    attn_combine_kernel<64><<<dim3(Hq, n, HD / 64), dim3(WAVE), 0, stream>>>(
+        part_o, part_ml, pos, Qg, ldp, Out, ldo, Hq, max_len, NS, ns_div(NS), v_scale);
   return hipGetLastError();
 }
 

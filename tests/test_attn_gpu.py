@@ -245,6 +245,21 @@ def test_multi_round_slices(native, hq, hkv, n, pos, ns):
         assert torch.equal(o1[0], out[t]), t
 
 
+@pytest.mark.parametrize("n,pos,ns", [(8, 3000, 200), (5, 777, 100), (6, 5000, 64), (8, 100, 3)])
+def test_combine_forms_agree(native, n, pos, ns):
+    """The combine runs in 32-dim chunks up to 768 waves (1-4 rows at GQA 6) and in 64-dim chunks
+    (two slice groups per lane) above: the two add in the same order, so row t of these n-row
+    calls (64-dim form) equals a 1-row call (32-dim form) bit for bit, also over several batches
+    of 64 slices (ns 100, 200) and with fewer slices than one batch (ns 3)."""
+    case = decode_case(seed=pos * 3 + n, hq=24, hkv=4, pos=pos, n=n, max_len=pos + n + 8)
+    out = gpu_decode(native, case, ns)
+    ok, mx, mean = attn_close(out, oracle_decode(case))
+    assert ok, (mx, mean)
+    for t in range(n):
+        o1 = gpu_decode(native, case, ns, pos=case.pos + t, rows=slice(t, t + 1))
+        assert torch.equal(o1[0], out[t]), t
+
+
 @pytest.mark.parametrize("n", [3, 5])
 def test_two_tile_kernels_give_the_same_bits(native, n):
     """3-5 rows (two MFMA column tiles) take the multi-column kernel when every slice of the cache
