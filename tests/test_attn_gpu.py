@@ -246,11 +246,11 @@ def test_multi_round_slices(native, hq, hkv, n, pos, ns):
 
 
 @pytest.mark.parametrize("n,pos,ns", [(8, 3000, 200), (5, 777, 100), (6, 5000, 64), (8, 100, 3)])
-def test_combine_forms_agree(native, n, pos, ns):
-    """The combine runs in 32-dim chunks up to 768 waves (1-4 rows at GQA 6) and in 64-dim chunks
-    (two slice groups per lane) above: the two add in the same order, so row t of these n-row
-    calls (64-dim form) equals a 1-row call (32-dim form) bit for bit, also over several batches
-    of 64 slices (ns 100, 200) and with fewer slices than one batch (ns 3)."""
+def test_combine_batches_and_rows(native, n, pos, ns):
+    """The combine merges slices in batches of 64 (16 lane groups of 4 slices, a fixed tree across
+    the groups, the running max rescaling between batches): several batches (ns 100, 200), one
+    full batch and fewer slices than one batch (ns 3) match the oracle, and row t of the n-row
+    call equals a 1-row call bit for bit."""
     case = decode_case(seed=pos * 3 + n, hq=24, hkv=4, pos=pos, n=n, max_len=pos + n + 8)
     out = gpu_decode(native, case, ns)
     ok, mx, mean = attn_close(out, oracle_decode(case))
