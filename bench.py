@@ -82,6 +82,12 @@ class LayerSet:
             self.C.attn_decode_partials(self.q, k, v, self.pos, self.qg, self.po, self.pml,
                                         self.out)
 
+    def combine_all(self):
+        """The combine alone, LAYERS times on the partials of the last layer-call."""
+        for k, v in zip(self.kc, self.vc):
+            self.C.attn_decode_combine(self.q, k, v, self.pos, self.qg, self.po, self.pml,
+                                       self.out)
+
 
 def fp8_codes(torch, shape, gen):
     """E4M3FN codes of N(0,1) values at scale 1/16 (code = RNE(16 x), saturated at 448)."""
@@ -209,8 +215,9 @@ def warm_device(torch, seconds: float = 1.0) -> float:
 
 def bench_length(torch, C, qa, L: int, steps: int, warmup: int, ns: int | None):
     """Layer-calls at KV length L (16 per graph on distinct caches, >= 512 MB in rotation): the
-    whole op, its partials kernel alone, and the two ceilings measured the same way: the
-    streaming probe on the partials grid (the K/V bytes, no arithmetic) and an empty launch."""
+    whole op, its partials kernel alone, its combine alone (on partials already written), and
+    the two ceilings measured the same way: the streaming probe on the partials grid (the K/V
+    bytes, no arithmetic) and an empty launch."""
     import qengine_amd.capi as capi
     ns = ns or qa.default_splits(L, HKV)
     nsets = max(1, math.ceil(ROTATE_BYTES / (LAYERS * L * 4096)))
@@ -224,9 +231,11 @@ def bench_length(torch, C, qa, L: int, steps: int, warmup: int, ns: int | None):
     full = [capture(torch, s.decode_all) for s in sets]
     part = [capture(torch, s.partials_all) for s in sets]
     probe = [capture(torch, lambda s=s: probe_all(s)) for s in sets]
+    comb = [capture(torch, s.combine_all) for s in sets]
     t_full = time_graphs(torch, full, steps, warmup)
     t_part = time_graphs(torch, part, steps, warmup)
     t_probe = time_graphs(torch, probe, steps, warmup)
+    t_comb = time_graphs(torch, comb, steps, warmup)
     us_layer = t_full.median * 1e3 / LAYERS
     us_part = t_part.median * 1e3 / LAYERS
     us_probe = t_probe.median * 1e3 / LAYERS
@@ -240,10 +249,11 @@ def bench_length(torch, C, qa, L: int, steps: int, warmup: int, ns: int | None):
         "partials_GBps": alg_bytes_partials(L) / (us_part * 1e3),
         "partials_us_mean": t_part.mean * 1e3 / LAYERS,
         "kv_stream_probe_us": us_probe,
+        "combine_us": t_comb.median * 1e3 / LAYERS,
     }
     res["frac"] = res["GBps"] / HBM_PEAK_GBS
     res["partials_frac"] = res["partials_GBps"] / HBM_PEAK_GBS
-    del sets, full, part, probe
+    del sets, full, part, probe, comb
     torch.cuda.empty_cache()
     return res
 
@@ -251,8 +261,9 @@ def bench_length(torch, C, qa, L: int, steps: int, warmup: int, ns: int | None):
 def ceiling(sweep, node_us: float) -> dict:
     """What any design can reach on this box, per KV length, in µs per layer-call: the streaming
     probe on the partials grid is the floor of one launch that reads the K/V bytes; adding one
-    empty graph node gives the floor of a two-launch layer-call (partials + combine); the
-    BASELINE target is 75% of 8 TB/s on the algorithmic bytes."""
+    empty graph node gives the floor of a two-launch layer-call (partials + combine), and the
+    combine alone is what this build's second node costs; the BASELINE target is 75% of 8 TB/s
+    on the algorithmic bytes."""
     out = {"graph_node_us": round(node_us, 3), "per_L": {}}
     for r in sweep:
         L = r["L"]
@@ -261,6 +272,7 @@ def ceiling(sweep, node_us: float) -> dict:
             "one_launch_floor_us": round(r["kv_stream_probe_us"], 3),
             "two_launch_floor_us": round(r["kv_stream_probe_us"] + node_us, 3),
             "measured_us": round(r["us_per_layer"], 3),
+            "combine_alone_us": round(r["combine_us"], 3),
             "target_75pct_us": round(alg_bytes_layer(L) / (0.75 * HBM_PEAK_GBS * 1e3), 3)}
     return out
 
