@@ -27,7 +27,8 @@
 //    layout that balances the causal triangle: 12 waves (three per SIMD) own one KV head and the
 //    16-row blocks j and nb-1-j of all six q heads, so every workgroup carries about the same
 //    work and the grid is one round of workgroups (config 5: 256). Same bits as the 8-wave
-//    kernel; 222 -> 212 us at config 5 (same-box A/B).
+//    kernel; 222 -> 212 us at config 5 (same-box A/B), and 211 -> 205 with one wave per SIMD
+//    running its tile phases shifted by one step.
 #include "attn_tile.hpp"
 #include "qe_attn.h"
 
@@ -297,8 +298,63 @@ attn_prefill_kernel(const __bf16* __restrict__ q, const void* __restrict__ kc,
 // for every j) for all 6 q heads of the group. Waves 0-5 take block j of heads 0-5, waves 6-11
 // block nb-1-j. Every workgroup then carries about the same work, and Hkv * nb/2 of them fill the
 // CUs in one round (256 at config 5). The first 8 waves load the K/V ring as in the 8-wave kernel.
+//
+// Phase shift: the per-tile barrier keeps all waves in the same phase, so a SIMD's MFMA, LDS and
+// VALU work run nearly in series. Waves 8-11 (the third wave of each SIMD, heavy blocks) run
+// iteration j as PV(j-1), QK(j), softmax(j), carrying P(j) to the next iteration, so their
+// softmax overlaps the other two waves' PV MFMAs and their PV(j-1) the others' softmax. Every
+// wave's accumulators see the same operations in the same order (PV(j-1) precedes softmax(j)'s
+// rescale either way), so the bits are unchanged. Tile j-1 must stay resident through iteration
+// j, so this kernel loads 2 tiles ahead in the 4-stage ring. Same-box A/B at config 5: 210.7 ->
+// 205.0 us (2 ahead alone: 211.8; shifting waves 4-7 or 0-3 instead: slower or 1% faster; two
+// shifted waves per SIMD: 212.5).
 constexpr int BAL_WAVES = 12;
 constexpr int BAL_GRP = 6;
+constexpr int BAL_AHEAD = 2;
+constexpr int BAL_SHIFT_FROM = 8;  // waves 8-11: one per SIMD
+
+template <bool SPLIT, bool MASK, bool SHIFTED>
+__device__ __forceinline__ void run_tiles_bal(int j0, int j1, int Lwave, u32x4_t* lds,
+                                              __amdgpu_buffer_rsrc_t krs,
+                                              __amdgpu_buffer_rsrc_t vrs, int w, int lane, int c,
+                                              int g4, const bf16x8_t (&qb)[NT][8],
+                                              const int (&Lcol)[NT], float scale_log2,
+                                              WaveState& st, bool& pend, u32x4_t (&ph)[NT],
+                                              u32x4_t (&pl)[NT]) {
+  static_assert(BAL_AHEAD <= STAGES - 2, "tile j-1 stays resident through iteration j");
+  for (int j = j0; j < j1; ++j) {
+    const u32x4_t* kt = lds + (j % STAGES) * STAGE_U4;
+    const u32x4_t* vt = kt + TILE_U4;
+    const int p0 = j * BN;
+    vmcnt_wait<LOADS_PER_TILE * (BAL_AHEAD - 1)>();  // this wave's loads of tile j are done
+    __syncthreads();  // ... and every wave's; tile j-2's stage is free
+    if (w < WAVES)
+      issue_tile(lds + ((j + BAL_AHEAD) % STAGES) * STAGE_U4, krs, vrs, p0 + BAL_AHEAD * BN, w,
+                 lane);
+    if (SHIFTED && pend) {  // PV of the previous tile
+      tile::pv_tile_tr<NT, SPLIT>(lds + ((j + STAGES - 1) % STAGES) * STAGE_U4 + TILE_U4, lane,
+                                  g4, ph, pl, st.acc);
+      pend = false;
+    }
+    if (p0 >= Lwave) continue;
+    f32x4_t sacc[NT][2];
+    tile::qk_tile<NT>(kt, qb, c, g4, sacc);
+    u32x4_t pb_hi[NT], pb_lo[NT];
+    tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc, pb_hi,
+                                        pb_lo);
+    if constexpr (SHIFTED) {
+#pragma unroll
+      for (int u = 0; u < NT; ++u) {
+        ph[u] = pb_hi[u];
+        pl[u] = pb_lo[u];
+      }
+      pend = true;
+    } else {
+      tile::pv_tile_tr<NT, SPLIT>(vt, lane, g4, pb_hi, pb_lo, st.acc);
+    }
+  }
+}
+
 __global__ void __launch_bounds__(BAL_WAVES * WAVE)
 attn_prefill_bal_kernel(const __bf16* __restrict__ q, const void* __restrict__ kc,
                         const void* __restrict__ vc, const int* __restrict__ pos_ptr,
@@ -359,15 +415,35 @@ attn_prefill_bal_kernel(const __bf16* __restrict__ q, const void* __restrict__ k
   const int jm = min(ntiles, max(Lmin, 0) / BN);
   if (w < WAVES) {
 #pragma unroll
-    for (int a = 0; a < AHEAD; ++a) issue_tile(lds + a * STAGE_U4, krs, vrs, a * BN, w, lane);
+    for (int a = 0; a < BAL_AHEAD; ++a) issue_tile(lds + a * STAGE_U4, krs, vrs, a * BN, w, lane);
   }
-  if (split) {
-    run_tiles<true, false>(0, jm, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol, scale_log2, st);
-    run_tiles<true, true>(jm, ntiles, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol, scale_log2, st);
-  } else {
-    run_tiles<false, false>(0, jm, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol, scale_log2, st);
-    run_tiles<false, true>(jm, ntiles, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol, scale_log2, st);
-  }
+  bool pend = false;  // a shifted wave's P of the previous tile is waiting for its PV
+  u32x4_t ph[NT], pl[NT];
+  // one code path per shift (a runtime flag inside the loop costs registers and spills)
+  auto tiles = [&](auto shifted) __attribute__((always_inline)) {
+    constexpr bool SH = decltype(shifted)::value;
+    if (split) {
+      run_tiles_bal<true, false, SH>(0, jm, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol,
+                                     scale_log2, st, pend, ph, pl);
+      run_tiles_bal<true, true, SH>(jm, ntiles, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol,
+                                    scale_log2, st, pend, ph, pl);
+      if (SH && pend)  // the last tile's PV (its stage is not refilled after the loop)
+        tile::pv_tile_tr<NT, true>(lds + ((ntiles - 1) % STAGES) * STAGE_U4 + TILE_U4, lane, g4,
+                                   ph, pl, st.acc);
+    } else {
+      run_tiles_bal<false, false, SH>(0, jm, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol,
+                                      scale_log2, st, pend, ph, pl);
+      run_tiles_bal<false, true, SH>(jm, ntiles, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol,
+                                     scale_log2, st, pend, ph, pl);
+      if (SH && pend)
+        tile::pv_tile_tr<NT, false>(lds + ((ntiles - 1) % STAGES) * STAGE_U4 + TILE_U4, lane, g4,
+                                    ph, pl, st.acc);
+    }
+  };
+  if (w >= BAL_SHIFT_FROM)
+    tiles(std::integral_constant<bool, true>{});
+  else
+    tiles(std::integral_constant<bool, false>{});
   vmcnt_wait<0>();  // no LDS DMA may still target this workgroup's LDS when it exits
 
   if (!wave_live || r >= T) return;
