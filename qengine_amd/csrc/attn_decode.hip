@@ -842,18 +842,18 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
   if (!attendA && !(npass > 1 && PB.beg < PB.end)) return;  // uniform per workgroup
 
   // fp8 with one column tile per wave: each subset's region also holds an 8 KB fp8 staging
-  // buffer (4 x 40 KB: all 160 KB of LDS), and s_m / s_l live in the ring past the merge's
-  // accumulators (the ring is idle once the rounds end).
+  // buffer (4 x 40 KB: all 160 KB of LDS), and s_m / s_l live in the ring past the merge's two
+  // accumulator buffers (the ring is idle once the rounds end).
   constexpr bool LA8 = KV8 && CPW == 1;
   constexpr int REGION = LA8 ? cols::REGION_U4 + cols::STAGE8_U4 : cols::REGION_U4;
   __shared__ __attribute__((aligned(16))) u32x4_t lds[SUB * REGION];  // 128 KB or 160 KB
   __shared__ float s_m_[LA8 ? 1 : SUB][16 * NT], s_l_[LA8 ? 1 : SUB][16 * NT];
-  static_assert(!LA8 || SUB * 16 * WAVE * 16 + 2 * SUB * 16 * NT * 4 <= SUB * REGION * 16,
-                "s_m and s_l fit the ring past the merge buffer");
+  static_assert(!LA8 || 2 * SUB * 16 * WAVE * 16 + 2 * SUB * 16 * NT * 4 <= SUB * REGION * 16,
+                "s_m and s_l fit the ring past the two merge buffers");
   float (*s_m)[16 * NT] =
-      LA8 ? reinterpret_cast<float (*)[16 * NT]>(lds + SUB * 16 * WAVE) : s_m_;
+      LA8 ? reinterpret_cast<float (*)[16 * NT]>(lds + 2 * SUB * 16 * WAVE) : s_m_;
   float (*s_l)[16 * NT] =
-      LA8 ? reinterpret_cast<float (*)[16 * NT]>(lds + SUB * 16 * WAVE) + SUB : s_l_;
+      LA8 ? reinterpret_cast<float (*)[16 * NT]>(lds + 2 * SUB * 16 * WAVE) + SUB : s_l_;
   constexpr int ELEM = KV8 ? 1 : 2;  // bytes per cache value
   const size_t head_off = (size_t)g * max_len * HD * ELEM;  // bytes
   u32x4_t* kt = lds + sub * REGION;
@@ -1071,26 +1071,39 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
         ml[1] = L;
       }
     }
-    f32x4_t (*s_acc)[16][WAVE] = reinterpret_cast<f32x4_t (*)[16][WAVE]>(lds);
-    static_assert(SUB * 16 * WAVE * 16 <= SUB * cols::REGION_U4 * 16, "merge buffer fits the ring");
-    for (int rr = 0; rr < WPS; ++rr) {
+    // The (rank, column tile) items are merged two at a time: each item's accumulators from the 4
+    // subsets take 64 KB, and two fill the ring, so one barrier pair serves both (3-4 rows at
+    // GQA 6: all of them). Thread (sub, lane) of an item's owner rank merges accumulators
+    // 4 sub .. 4 sub + 3 over the subsets in order 0..3.
+    constexpr int GROUP = 2;
+    constexpr int NI = WPS * CPW;  // items, rank-major within each column tile u
+    static_assert(GROUP * SUB * 16 * WAVE * 16 <= SUB * cols::REGION_U4 * 16,
+                  "two items' merge buffers fit the ring");
+    f32x4_t (*s_acc)[SUB][16][WAVE] = reinterpret_cast<f32x4_t (*)[SUB][16][WAVE]>(lds);
 #pragma unroll
-      for (int u = 0; u < CPW; ++u) {
-        const int col = (rr * CPW + u) * 16 + c;
-        const bool mine = rank == rr && in_pass(col, grp, P);
-        if (mine) {
+    for (int i0 = 0; i0 < NI; i0 += GROUP) {
 #pragma unroll
-          for (int a = 0; a < 16; ++a) s_acc[sub][a][lane] = acc[u][a];
+      for (int gi = 0; gi < GROUP; ++gi) {
+        if (i0 + gi >= NI) break;
+        const int u = (i0 + gi) / WPS, rr = (i0 + gi) % WPS;
+        if (rank == rr && in_pass((rr * CPW + u) * 16 + c, grp, P)) {
+#pragma unroll
+          for (int a = 0; a < 16; ++a) s_acc[gi][sub][a][lane] = acc[u][a];
         }
-        __syncthreads();
-        if (mine) {
-          // thread (sub, lane) merges accumulators 4 sub .. 4 sub + 3 over the subsets in order
+      }
+      __syncthreads();
+#pragma unroll
+      for (int gi = 0; gi < GROUP; ++gi) {
+        if (i0 + gi >= NI) break;
+        const int u = (i0 + gi) / WPS, rr = (i0 + gi) % WPS;
+        const int col = (rr * CPW + u) * 16 + c;
+        if (rank == rr && in_pass(col, grp, P)) {
           f32x4_t mo[4];
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             f32x4_t sum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int v = 0; v < SUB; ++v) sum += s_acc[v][4 * sub + k][lane] * wsc[u][v];
+            for (int v = 0; v < SUB; ++v) sum += s_acc[gi][v][4 * sub + k][lane] * wsc[u][v];
             mo[k] = sum;
           }
           const int t = col / grp, head = g * grp + (col - t * grp);
@@ -1100,8 +1113,8 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
           for (int k = 0; k < 4; ++k)
             reinterpret_cast<f32x4_t*>(dst + 16 * (4 * sub + k) + 4 * g4)[0] = mo[k];
         }
-        __syncthreads();  // (also ends the pass: the next pass's loads may overwrite `lds`)
       }
+      __syncthreads();  // (also ends the pass: the next pass's loads may overwrite `lds`)
     }
   };
   if (attendA) run_pass(PA);
