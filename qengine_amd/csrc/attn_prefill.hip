@@ -355,11 +355,60 @@ __device__ __forceinline__ void run_tiles_bal(int j0, int j1, int Lwave, u32x4_t
   }
 }
 
+// run_tiles_bal on the fp8 cache: the fp8 ring and the double-buffered bf16 pair of
+// run_tiles8, converted by the first 8 waves (512 threads, one 16-byte chunk of K and of V each).
+// A shifted wave's PV of tile j-1 reads pair (j-1) % 2, which the conversion of iteration j+1
+// rewrites only after that iteration's barrier, so the fp8 ring keeps loading 3 tiles ahead.
+template <bool SPLIT, bool MASK, bool SHIFTED>
+__device__ __forceinline__ void run_tiles_bal8(int j0, int j1, int Lwave, u32x4_t* lds,
+                                               __amdgpu_buffer_rsrc_t krs,
+                                               __amdgpu_buffer_rsrc_t vrs, int w, int lane, int c,
+                                               int g4, const bf16x8_t (&qb)[NT][8],
+                                               const int (&Lcol)[NT], float scale_log2,
+                                               WaveState& st, bool& pend, u32x4_t (&ph)[NT],
+                                               u32x4_t (&pl)[NT]) {
+  u32x4_t* bfp = lds + STAGES * STAGE8_U4;
+  for (int j = j0; j < j1; ++j) {
+    const int p0 = j * BN;
+    vmcnt_wait<LOADS_PER_TILE8 * (AHEAD - 1)>();  // this wave's loads of tile j are done
+    __syncthreads();  // ... and every wave's; tile j-1's fp8 stage and pair j % 2 are free
+    if (w < WAVES) {
+      issue_tile8(lds + ((j + AHEAD) % STAGES) * STAGE8_U4, krs, vrs, p0 + AHEAD * BN, w, lane);
+      convert_tile8(lds + (j % STAGES) * STAGE8_U4, bfp + (j & 1) * STAGE_U4);
+    }
+    lds_barrier();  // the bf16 tile is complete
+    if (SHIFTED && pend) {  // PV of the previous tile, from the other pair
+      tile::pv_tile_tr<NT, SPLIT>(bfp + ((j + 1) & 1) * STAGE_U4 + TILE_U4, lane, g4, ph, pl,
+                                  st.acc);
+      pend = false;
+    }
+    if (p0 >= Lwave) continue;
+    const u32x4_t* bf = bfp + (j & 1) * STAGE_U4;
+    f32x4_t sacc[NT][2];
+    tile::qk_tile<NT>(bf, qb, c, g4, sacc);
+    u32x4_t pb_hi[NT], pb_lo[NT];
+    tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc, pb_hi,
+                                        pb_lo);
+    if constexpr (SHIFTED) {
+#pragma unroll
+      for (int u = 0; u < NT; ++u) {
+        ph[u] = pb_hi[u];
+        pl[u] = pb_lo[u];
+      }
+      pend = true;
+    } else {
+      tile::pv_tile_tr<NT, SPLIT>(bf + TILE_U4, lane, g4, pb_hi, pb_lo, st.acc);
+    }
+  }
+}
+
+template <bool KV8>
 __global__ void __launch_bounds__(BAL_WAVES * WAVE)
 attn_prefill_bal_kernel(const __bf16* __restrict__ q, const void* __restrict__ kc,
                         const void* __restrict__ vc, const int* __restrict__ pos_ptr,
                         const __bf16* __restrict__ qg, long ldp, __bf16* __restrict__ out, long ldo,
-                        int T, int Hq, int Hkv, int max_len, float scale_log2, int xcd_split) {
+                        int T, int Hq, int Hkv, int max_len, float scale_log2, float v_scale,
+                        int xcd_split) {
   const int nb = (T + 15) / 16, npairs = (nb + 1) / 2;
   int g, jp;
   if (xcd_split > 0) {
@@ -401,8 +450,9 @@ attn_prefill_bal_kernel(const __bf16* __restrict__ q, const void* __restrict__ k
   const int ntiles = Lwg > 0 ? (Lwg + BN - 1) / BN : 0;
   const bool split = Lmin < SPLIT_BELOW;
 
-  const size_t head_off = (size_t)g * max_len * HD * 2;
-  const uint32_t bytes = (uint32_t)max(Lwg, 0) * (uint32_t)(HD * 2);
+  constexpr int ELEM = KV8 ? 1 : 2;  // bytes per cache value
+  const size_t head_off = (size_t)g * max_len * HD * ELEM;
+  const uint32_t bytes = (uint32_t)max(Lwg, 0) * (uint32_t)(HD * ELEM);
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(static_cast<const char*>(kc) + head_off, bytes);
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(static_cast<const char*>(vc) + head_off, bytes);
 
@@ -414,30 +464,44 @@ attn_prefill_bal_kernel(const __bf16* __restrict__ q, const void* __restrict__ k
 
   const int jm = min(ntiles, max(Lmin, 0) / BN);
   if (w < WAVES) {
+    if constexpr (KV8) {
 #pragma unroll
-    for (int a = 0; a < BAL_AHEAD; ++a) issue_tile(lds + a * STAGE_U4, krs, vrs, a * BN, w, lane);
+      for (int a = 0; a < AHEAD; ++a)
+        issue_tile8(lds + a * STAGE8_U4, krs, vrs, a * BN, w, lane);
+    } else {
+#pragma unroll
+      for (int a = 0; a < BAL_AHEAD; ++a)
+        issue_tile(lds + a * STAGE_U4, krs, vrs, a * BN, w, lane);
+    }
   }
   bool pend = false;  // a shifted wave's P of the previous tile is waiting for its PV
   u32x4_t ph[NT], pl[NT];
   // one code path per shift (a runtime flag inside the loop costs registers and spills)
+  // the V tile of the last tile (not refilled after the loop): its bf16 ring stage or pair
+  const u32x4_t* vlast =
+      KV8 ? lds + STAGES * STAGE8_U4 + ((ntiles - 1) & 1) * STAGE_U4 + TILE_U4
+          : lds + ((ntiles - 1) % STAGES) * STAGE_U4 + TILE_U4;
   auto tiles = [&](auto shifted) __attribute__((always_inline)) {
     constexpr bool SH = decltype(shifted)::value;
+    auto run = [&](auto sp, auto mk, int j0, int j1) __attribute__((always_inline)) {
+      constexpr bool SP = decltype(sp)::value, MK = decltype(mk)::value;
+      if constexpr (KV8)
+        run_tiles_bal8<SP, MK, SH>(j0, j1, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol,
+                                   scale_log2, st, pend, ph, pl);
+      else
+        run_tiles_bal<SP, MK, SH>(j0, j1, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol,
+                                  scale_log2, st, pend, ph, pl);
+    };
+    using T_ = std::integral_constant<bool, true>;
+    using F_ = std::integral_constant<bool, false>;
     if (split) {
-      run_tiles_bal<true, false, SH>(0, jm, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol,
-                                     scale_log2, st, pend, ph, pl);
-      run_tiles_bal<true, true, SH>(jm, ntiles, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol,
-                                    scale_log2, st, pend, ph, pl);
-      if (SH && pend)  // the last tile's PV (its stage is not refilled after the loop)
-        tile::pv_tile_tr<NT, true>(lds + ((ntiles - 1) % STAGES) * STAGE_U4 + TILE_U4, lane, g4,
-                                   ph, pl, st.acc);
+      run(T_{}, F_{}, 0, jm);
+      run(T_{}, T_{}, jm, ntiles);
+      if (SH && pend) tile::pv_tile_tr<NT, true>(vlast, lane, g4, ph, pl, st.acc);
     } else {
-      run_tiles_bal<false, false, SH>(0, jm, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol,
-                                      scale_log2, st, pend, ph, pl);
-      run_tiles_bal<false, true, SH>(jm, ntiles, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol,
-                                     scale_log2, st, pend, ph, pl);
-      if (SH && pend)
-        tile::pv_tile_tr<NT, false>(lds + ((ntiles - 1) % STAGES) * STAGE_U4 + TILE_U4, lane, g4,
-                                    ph, pl, st.acc);
+      run(F_{}, F_{}, 0, jm);
+      run(F_{}, T_{}, jm, ntiles);
+      if (SH && pend) tile::pv_tile_tr<NT, false>(vlast, lane, g4, ph, pl, st.acc);
     }
   };
   if (w >= BAL_SHIFT_FROM)
@@ -457,8 +521,9 @@ attn_prefill_bal_kernel(const __bf16* __restrict__ q, const void* __restrict__ k
     u32x2_t ob;
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const float o0 = round_bf16(st.acc[0][i][2 * k] / L);
-      const float o1 = round_bf16(st.acc[0][i][2 * k + 1] / L);
+      // v_scale: the fp8 cache's V scale, exactly 1 for the bf16 cache
+      const float o0 = round_bf16((st.acc[0][i][2 * k] / L) * v_scale);
+      const float o1 = round_bf16((st.acc[0][i][2 * k + 1] / L) * v_scale);
       const float s0 = round_bf16(sigmoid_f32(lo_bf16(gb[k])));
       const float s1 = round_bf16(sigmoid_f32(hi_bf16(gb[k])));
       ob[k] = pack_bf16x2(o0 * s0, o1 * s1);
@@ -496,11 +561,16 @@ static hipError_t launch_prefill(const void* q, const void* kc, const void* vc, 
   const auto* Q = static_cast<const __bf16*>(q);
   const auto* QG = static_cast<const __bf16*>(qg);
   auto* O = static_cast<__bf16*>(out);
-  if (!kv8 && Hq == prefill::BAL_GRP * Hkv) {  // balanced 12-wave layout (GQA 6, bf16 cache)
+  if (Hq == prefill::BAL_GRP * Hkv) {  // balanced 12-wave layout (GQA 6)
     const int nb = (T + 15) / 16, npairs = (nb + 1) / 2;
     const int xs = per_head > 0 && npairs % per_head == 0 ? per_head : 0;
-    prefill::attn_prefill_bal_kernel<<<dim3(npairs * Hkv), dim3(prefill::BAL_WAVES * WAVE), 0, stream>>>(
-        Q, kc, vc, pos, QG, ldp, O, ldo, T, Hq, Hkv, max_len, scale_log2, xs);
+    const dim3 bgrid(npairs * Hkv), bblock(prefill::BAL_WAVES * WAVE);
+    if (kv8)
+      prefill::attn_prefill_bal_kernel<true><<<bgrid, bblock, 0, stream>>>(
+          Q, kc, vc, pos, QG, ldp, O, ldo, T, Hq, Hkv, max_len, scale_log2, v_scale, xs);
+    else
+      prefill::attn_prefill_bal_kernel<false><<<bgrid, bblock, 0, stream>>>(
+          Q, kc, vc, pos, QG, ldp, O, ldo, T, Hq, Hkv, max_len, scale_log2, 1.f, xs);
     return hipGetLastError();
   }
   if (kv8)
