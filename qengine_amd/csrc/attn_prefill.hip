@@ -27,9 +27,13 @@
 //    layout that balances the causal triangle: 12 waves (three per SIMD) own one KV head and the
 //    16-row blocks j and nb-1-j of all six q heads, so every workgroup carries about the same
 //    work and the grid is one round of workgroups (config 5: 256). Same bits as the 8-wave
-//    kernel; 222 -> 212 us at config 5 (same-box A/B), and 211 -> 205 with one wave per SIMD
-//    running its tile phases shifted by one step. On the fp8 cache it replaced the 8-wave kernel
-//    at GQA 6: 290 -> 243 us.
+//    kernel; 222 -> 212 us at config 5 (same-box A/B). On the fp8 cache it replaced the 8-wave
+//    kernel at GQA 6: 290 -> 243 us.
+//  * The file is compiled with LLVM's max-ILP machine scheduler. Under the default
+//    (occupancy-first) scheduler the tile loop kept one LDS operand read in flight and waited
+//    for it before every MFMA; max-ILP interleaves the two S^T accumulation chains and keeps two
+//    or more reads in flight in the same 168 registers. Same bits; config 5, same-box A/B against
+//    the default scheduler: 207.8 -> 189.3 us (bf16 cache), 243.7 -> 224.7 us (fp8 cache).
 #include "attn_tile.hpp"
 #include "qe_attn.h"
 
@@ -298,91 +302,62 @@ attn_prefill_kernel(const __bf16* __restrict__ q, const void* __restrict__ kc,
 // of 16-row blocks j and nb-1-j (light and heavy: their attended lengths add up to about the same
 // for every j) for all 6 q heads of the group. Waves 0-5 take block j of heads 0-5, waves 6-11
 // block nb-1-j. Every workgroup then carries about the same work, and Hkv * nb/2 of them fill the
-// CUs in one round (256 at config 5). The first 8 waves load the K/V ring as in the 8-wave kernel.
-//
-// Phase shift: the per-tile barrier keeps all waves in the same phase, so a SIMD's MFMA, LDS and
-// VALU work run nearly in series. Waves 8-11 (the third wave of each SIMD, heavy blocks) run
-// iteration j as PV(j-1), QK(j), softmax(j), carrying P(j) to the next iteration, so their
-// softmax overlaps the other two waves' PV MFMAs and their PV(j-1) the others' softmax. Every
-// wave's accumulators see the same operations in the same order (PV(j-1) precedes softmax(j)'s
-// rescale either way), so the bits are unchanged. Tile j-1 must stay resident through iteration
-// j, so this kernel loads 2 tiles ahead in the 4-stage ring. Same-box A/B at config 5: 210.7 ->
-// 205.0 us (2 ahead alone: 211.8; shifting waves 4-7 or 0-3 instead: slower or 1% faster; two
-// shifted waves per SIMD: 212.5).
+// CUs in one round (256 at config 5). The first 8 waves load the K/V ring as in the 8-wave kernel,
+// 2 tiles ahead in the 4-stage ring (config 5 under the max-ILP scheduler: 189.3 us against 190.5
+// with 3 ahead).
 constexpr int BAL_WAVES = 12;
 constexpr int BAL_GRP = 6;
 constexpr int BAL_AHEAD = 2;
-constexpr int BAL_SHIFT_FROM = 8;  // waves 8-11: one per SIMD
 
-template <bool SPLIT, bool MASK, bool SHIFTED>
+// LOAD: this wave is one of the first 8, which fill the ring. The loaders and the other 4 waves
+// run separate copies of the loop, so neither carries the other's code (config 5: 212.8 -> 191.9
+// us on one box against the same loop with a per-wave branch around the loads, same bits).
+template <bool SPLIT, bool MASK, bool LOAD>
 __device__ __forceinline__ void run_tiles_bal(int j0, int j1, int Lwave, u32x4_t* lds,
                                               __amdgpu_buffer_rsrc_t krs,
                                               __amdgpu_buffer_rsrc_t vrs, int w, int lane, int c,
                                               int g4, const bf16x8_t (&qb)[NT][8],
                                               const int (&Lcol)[NT], float scale_log2,
-                                              WaveState& st, bool& pend, u32x4_t (&ph)[NT],
-                                              u32x4_t (&pl)[NT]) {
-  static_assert(BAL_AHEAD <= STAGES - 2, "tile j-1 stays resident through iteration j");
+                                              WaveState& st) {
   for (int j = j0; j < j1; ++j) {
     const u32x4_t* kt = lds + (j % STAGES) * STAGE_U4;
     const u32x4_t* vt = kt + TILE_U4;
     const int p0 = j * BN;
     vmcnt_wait<LOADS_PER_TILE * (BAL_AHEAD - 1)>();  // this wave's loads of tile j are done
-    __syncthreads();  // ... and every wave's; tile j-2's stage is free
-    if (w < WAVES)
+    __syncthreads();  // ... and every wave's; the stage refilled now (tile j-2's) is free
+    if (LOAD)
       issue_tile(lds + ((j + BAL_AHEAD) % STAGES) * STAGE_U4, krs, vrs, p0 + BAL_AHEAD * BN, w,
                  lane);
-    if (SHIFTED && pend) {  // PV of the previous tile
-      tile::pv_tile_tr<NT, SPLIT>(lds + ((j + STAGES - 1) % STAGES) * STAGE_U4 + TILE_U4, lane,
-                                  g4, ph, pl, st.acc);
-      pend = false;
-    }
     if (p0 >= Lwave) continue;
     f32x4_t sacc[NT][2];
     tile::qk_tile<NT>(kt, qb, c, g4, sacc);
     u32x4_t pb_hi[NT], pb_lo[NT];
     tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc, pb_hi,
                                         pb_lo);
-    if constexpr (SHIFTED) {
-#pragma unroll
-      for (int u = 0; u < NT; ++u) {
-        ph[u] = pb_hi[u];
-        pl[u] = pb_lo[u];
-      }
-      pend = true;
-    } else {
-      tile::pv_tile_tr<NT, SPLIT>(vt, lane, g4, pb_hi, pb_lo, st.acc);
-    }
+    tile::pv_tile_tr<NT, SPLIT>(vt, lane, g4, pb_hi, pb_lo, st.acc);
   }
 }
 
 // run_tiles_bal on the fp8 cache: the fp8 ring and the double-buffered bf16 pair of
-// run_tiles8, converted by the first 8 waves (512 threads, one 16-byte chunk of K and of V each).
-// A shifted wave's PV of tile j-1 reads pair (j-1) % 2, which the conversion of iteration j+1
-// rewrites only after that iteration's barrier, so the fp8 ring keeps loading 3 tiles ahead.
-template <bool SPLIT, bool MASK, bool SHIFTED>
+// run_tiles8, loaded and converted by the first 8 waves (LOAD; 512 threads, one 16-byte chunk of
+// K and of V each).
+template <bool SPLIT, bool MASK, bool LOAD>
 __device__ __forceinline__ void run_tiles_bal8(int j0, int j1, int Lwave, u32x4_t* lds,
                                                __amdgpu_buffer_rsrc_t krs,
                                                __amdgpu_buffer_rsrc_t vrs, int w, int lane, int c,
                                                int g4, const bf16x8_t (&qb)[NT][8],
                                                const int (&Lcol)[NT], float scale_log2,
-                                               WaveState& st, bool& pend, u32x4_t (&ph)[NT],
-                                               u32x4_t (&pl)[NT]) {
+                                               WaveState& st) {
   u32x4_t* bfp = lds + STAGES * STAGE8_U4;
   for (int j = j0; j < j1; ++j) {
     const int p0 = j * BN;
     vmcnt_wait<LOADS_PER_TILE8 * (AHEAD - 1)>();  // this wave's loads of tile j are done
     __syncthreads();  // ... and every wave's; tile j-1's fp8 stage and pair j % 2 are free
-    if (w < WAVES) {
+    if (LOAD) {
       issue_tile8(lds + ((j + AHEAD) % STAGES) * STAGE8_U4, krs, vrs, p0 + AHEAD * BN, w, lane);
       convert_tile8(lds + (j % STAGES) * STAGE8_U4, bfp + (j & 1) * STAGE_U4);
     }
     lds_barrier();  // the bf16 tile is complete
-    if (SHIFTED && pend) {  // PV of the previous tile, from the other pair
-      tile::pv_tile_tr<NT, SPLIT>(bfp + ((j + 1) & 1) * STAGE_U4 + TILE_U4, lane, g4, ph, pl,
-                                  st.acc);
-      pend = false;
-    }
     if (p0 >= Lwave) continue;
     const u32x4_t* bf = bfp + (j & 1) * STAGE_U4;
     f32x4_t sacc[NT][2];
@@ -390,16 +365,7 @@ __device__ __forceinline__ void run_tiles_bal8(int j0, int j1, int Lwave, u32x4_
     u32x4_t pb_hi[NT], pb_lo[NT];
     tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc, pb_hi,
                                         pb_lo);
-    if constexpr (SHIFTED) {
-#pragma unroll
-      for (int u = 0; u < NT; ++u) {
-        ph[u] = pb_hi[u];
-        pl[u] = pb_lo[u];
-      }
-      pend = true;
-    } else {
-      tile::pv_tile_tr<NT, SPLIT>(bf + TILE_U4, lane, g4, pb_hi, pb_lo, st.acc);
-    }
+    tile::pv_tile_tr<NT, SPLIT>(bf + TILE_U4, lane, g4, pb_hi, pb_lo, st.acc);
   }
 }
 
@@ -475,40 +441,32 @@ attn_prefill_bal_kernel(const __bf16* __restrict__ q, const void* __restrict__ k
         issue_tile(lds + a * STAGE_U4, krs, vrs, a * BN, w, lane);
     }
   }
-  bool pend = false;  // a shifted wave's P of the previous tile is waiting for its PV
-  u32x4_t ph[NT], pl[NT];
-  // one code path per shift (a runtime flag inside the loop costs registers and spills)
-  // the V tile of the last tile (not refilled after the loop): its bf16 ring stage or pair
-  const u32x4_t* vlast =
-      KV8 ? lds + STAGES * STAGE8_U4 + ((ntiles - 1) & 1) * STAGE_U4 + TILE_U4
-          : lds + ((ntiles - 1) % STAGES) * STAGE_U4 + TILE_U4;
-  auto tiles = [&](auto shifted) __attribute__((always_inline)) {
-    constexpr bool SH = decltype(shifted)::value;
-    auto run = [&](auto sp, auto mk, int j0, int j1) __attribute__((always_inline)) {
-      constexpr bool SP = decltype(sp)::value, MK = decltype(mk)::value;
-      if constexpr (KV8)
-        run_tiles_bal8<SP, MK, SH>(j0, j1, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol,
-                                   scale_log2, st, pend, ph, pl);
+  // one branch-free loop body per (split, mask) case
+  auto run = [&](auto sp, auto mk, int j0, int j1) __attribute__((always_inline)) {
+    constexpr bool SP = decltype(sp)::value, MK = decltype(mk)::value;
+    if constexpr (KV8) {
+      if (w < WAVES)
+        run_tiles_bal8<SP, MK, true>(j0, j1, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol,
+                                     scale_log2, st);
       else
-        run_tiles_bal<SP, MK, SH>(j0, j1, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol,
-                                  scale_log2, st, pend, ph, pl);
-    };
-    using T_ = std::integral_constant<bool, true>;
-    using F_ = std::integral_constant<bool, false>;
-    if (split) {
-      run(T_{}, F_{}, 0, jm);
-      run(T_{}, T_{}, jm, ntiles);
-      if (SH && pend) tile::pv_tile_tr<NT, true>(vlast, lane, g4, ph, pl, st.acc);
-    } else {
-      run(F_{}, F_{}, 0, jm);
-      run(F_{}, T_{}, jm, ntiles);
-      if (SH && pend) tile::pv_tile_tr<NT, false>(vlast, lane, g4, ph, pl, st.acc);
-    }
+        run_tiles_bal8<SP, MK, false>(j0, j1, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol,
+                                      scale_log2, st);
+    } else if (w < WAVES)
+      run_tiles_bal<SP, MK, true>(j0, j1, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol,
+                                  scale_log2, st);
+    else
+      run_tiles_bal<SP, MK, false>(j0, j1, Lwave, lds, krs, vrs, w, lane, c, g4, qb, Lcol,
+                                   scale_log2, st);
   };
-  if (w >= BAL_SHIFT_FROM)
-    tiles(std::integral_constant<bool, true>{});
-  else
-    tiles(std::integral_constant<bool, false>{});
+  using T_ = std::integral_constant<bool, true>;
+  using F_ = std::integral_constant<bool, false>;
+  if (split) {
+    run(T_{}, F_{}, 0, jm);
+    run(T_{}, T_{}, jm, ntiles);
+  } else {
+    run(F_{}, F_{}, 0, jm);
+    run(F_{}, T_{}, jm, ntiles);
+  }
   vmcnt_wait<0>();  // no LDS DMA may still target this workgroup's LDS when it exits
 
   if (!wave_live || r >= T) return;
