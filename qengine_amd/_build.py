@@ -26,16 +26,18 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["attn_prep.hip", "attn_decode.hip", "attn_combine.hip", "attn_prefill.hip",
-               "gemv.hip", "step.hip", "gdn.hip"]
+               "gemv.hip", "gemv_lds.hip", "step.hip", "gdn.hip", "gdn_split.hip"]
 # Per-source code-generation flags. The prefill tile loop keeps 128 fp32 accumulators live; the
 # compiler's default MFMA register form parks them in AGPRs and copies all of them into VGPRs
 # on every iteration. The VGPR form keeps them in place. The max-ILP machine scheduler keeps
 # two or more LDS operand reads in flight in the tile loop where the default occupancy-first
 # scheduler kept one (same code, same bits; config 5 about 9% faster).
-# The decode combine is scheduled the same way (its partials kernels measured slower under it).
+# The decode combine, the Gated DeltaNet split path and the 1-2-row GEMV are scheduled the same
+# way; the kernels that measured slower under it (decode partials, the one-workgroup Gated
+# DeltaNet step, the 3-8-row GEMV) sit in files of their own with the default.
 MAX_ILP = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
 SOURCE_FLAGS = {"attn_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", *MAX_ILP],
-                "attn_combine.hip": MAX_ILP}
+                "attn_combine.hip": MAX_ILP, "gdn_split.hip": MAX_ILP, "gemv_lds.hip": MAX_ILP}
 LIB = PKG / "libqe_attn.so"
 EXT = PKG / ("_C" + sysconfig.get_config_var("EXT_SUFFIX"))
 

@@ -20,123 +20,15 @@
 //    and measured 47% of HBM peak vs 77% this way (in_proj, 1 row, MI355X). The chunks are
 //    XOR-swizzled by row, so the ds_read_b128 of an operand is bank-conflict free.
 //  * 3-8 rows load the activation rows into registers instead (gemv_bf16_xr_kernel), so the LDS
-//    ring stays small enough for two workgroups per CU.
+//    ring stays small enough for two workgroups per CU. The LDS-staged kernel for 1-2 rows
+//    (gemv_bf16_kernel) is in gemv_lds.hip, compiled with the max-ILP scheduler.
 //  * A workgroup holds 4 waves = 4/S row tiles x S k-parts; S grows as N shrinks so small
 //    projections still keep the CUs streaming. The S partial sums are added through LDS in the
 //    fixed order 0..S-1, so results never depend on timing.
-#include "qe_device.hpp"
+#include "gemv_common.hpp"
 #include "qe_gemv.h"
 
 namespace qe {
-
-constexpr int GEMV_WAVES = 4;
-constexpr int GEMV_STG = 2;       // ring stages per wave
-constexpr int GEMV_KB = 256;      // k per block (one stage)
-constexpr int GEMV_W_SLOTS = 16 * (GEMV_KB / 8);  // 16-byte slots of a W block: 512
-
-template <int XI>
-constexpr int gemv_stage_slots() { return GEMV_W_SLOTS + 64 * XI; }
-template <int XI>
-constexpr size_t gemv_lds_bytes() {
-  return (size_t)GEMV_WAVES * GEMV_STG * gemv_stage_slots<XI>() * 16;
-}
-
-// XI: LDS-DMA instructions of activation rows per block (two rows each, nr <= 2 * XI).
-template <int S, int XI>
-__global__ void __launch_bounds__(GEMV_WAVES * WAVE)
-gemv_bf16_kernel(const __bf16* __restrict__ W, const __bf16* __restrict__ x,
-                 __bf16* __restrict__ out, int nr, int N, int K, long ldx, long ldo) {
-  constexpr int RT = GEMV_WAVES / S;  // row tiles per workgroup
-  constexpr int SLOTS = gemv_stage_slots<XI>();
-  constexpr int LPS = GEMV_W_SLOTS / 64 + XI;  // loads per stage
-  extern __shared__ __attribute__((aligned(16))) u32x4_t gemv_smem[];
-  const int lane = threadIdx.x & (WAVE - 1);
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
-  const int i = lane & 15, g4 = lane >> 4;
-  const int tile = blockIdx.x * RT + w / S, kp = w % S;
-  const int r0 = tile * 16;
-  // A tile past N (only in the last workgroup) loads nothing but still meets the barrier below.
-  const bool live = r0 < N;
-
-  const int K8 = K >> 3;                              // 16-byte chunks per row
-  const int nblk = (K + GEMV_KB - 1) / GEMV_KB;       // 256-k blocks per row (last may be partial)
-  const int b_beg = kp * nblk / S, b_end = live ? (kp + 1) * nblk / S : b_beg;
-  const uint32_t tile_bytes = live ? (uint32_t)min(16, N - r0) * (uint32_t)K * 2u : 0u;
-  const __amdgpu_buffer_rsrc_t wrs = make_rsrc_uniform(W + (size_t)r0 * K, tile_bytes);
-  const __amdgpu_buffer_rsrc_t xrs =
-      make_rsrc_uniform(x, (uint32_t)(((size_t)(nr - 1) * ldx + K) * 2));
-  u32x4_t* ring = gemv_smem + (size_t)w * GEMV_STG * SLOTS;
-
-  // Slot (r, q) of a stage holds chunk q ^ (r & 15) of row r; rows and chunks past the matrix
-  // read 0 (buffer bounds) or are zeroed at use (chunks past K in a partial last block).
-  auto issue = [&](int blk, int st) {
-    u32x4_t* sb = ring + st * SLOTS;
-#pragma unroll
-    for (int j = 0; j < GEMV_W_SLOTS / 64; ++j) {
-      const int r = 2 * j + (lane >> 5), q = lane & 31;
-      buffer_load16_to_lds(wrs, (uint32_t)r * (uint32_t)K * 2u +
-                                    (uint32_t)(blk * GEMV_KB + (q ^ (r & 15)) * 8) * 2u,
-                           sb + 64 * j);
-    }
-#pragma unroll
-    for (int j = 0; j < XI; ++j) {
-      const int c = 2 * j + (lane >> 5), q = lane & 31;
-      const int cr = c < nr ? c : nr - 1;
-      buffer_load16_to_lds<0>(xrs, (uint32_t)(cr * ldx + blk * GEMV_KB + (q ^ (c & 15)) * 8) * 2u,
-                              sb + GEMV_W_SLOTS + 64 * j);
-    }
-  };
-
-  const bool xok = i < nr;
-  const int xr = i < 2 * XI ? i : 2 * XI - 1;  // staged activation row this lane reads
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  const int nb = b_end - b_beg;
-  if (nb > 0) issue(b_beg, 0);
-  for (int t = 0; t < nb; ++t) {
-    // the next block goes in flight before this one is waited for
-    if (t + 1 < nb) {
-      issue(b_beg + t + 1, (t + 1) % GEMV_STG);
-      vmcnt_wait<LPS>();
-    } else {
-      vmcnt_wait<0>();
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    const u32x4_t* sb = ring + (t % GEMV_STG) * SLOTS;
-    const int cbase = (b_beg + t) * (GEMV_KB / 8);    // first chunk of this block
-#pragma unroll
-    for (int ks = 0; ks < GEMV_KB / 32; ++ks) {
-      const int q = 4 * ks + g4;
-      const bool ok = cbase + q < K8;
-      const u32x4_t z = {0u, 0u, 0u, 0u};
-      const u32x4_t a = sb[i * 32 + (q ^ i)];
-      const u32x4_t b = sb[GEMV_W_SLOTS + xr * 32 + (q ^ xr)];
-      acc = mfma16x16x32(as_bf16x8(ok ? a : z), as_bf16x8(ok && xok ? b : z), acc);
-    }
-    // this stage's LDS reads are complete (their values fed the MFMAs) before the DMA that
-    // refills it is issued in the next iteration
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-  }
-
-  if constexpr (S > 1) {
-    __shared__ f32x4_t red[GEMV_WAVES][WAVE];
-    red[w][lane] = acc;
-    __syncthreads();
-    if (kp != 0) return;
-#pragma unroll
-    for (int v = 1; v < S; ++v) acc += red[w + v][lane];  // ((p0 + p1) + p2) + ...
-  }
-  // lane (g4, c = i) holds out^T rows r0 + 4g4 + j, column c
-  if (i < nr) {
-    __bf16* op = out + (size_t)i * ldo;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = r0 + 4 * g4 + j;
-      if (row < N) op[row] = f32_to_bf16(acc[j]);
-    }
-  }
-}
 
 // 3-8 activation rows: the same kernel with the activation rows loaded straight into registers in
 // the MFMA B-operand layout (lane 16*g4 + c: row c, k = 32*ks + 8*g4 + [0, 8) of the block), 8
@@ -267,23 +159,6 @@ hbm_read_probe_kernel(const u32x4_t* __restrict__ p, size_t n16, uint32_t* __res
   if (acc == 0x9E3779B9u) sink[0] = acc;
 }
 
-template <int S, int XI>
-static hipError_t launch_gemv(const __bf16* W, const __bf16* x, __bf16* out, int nr, int N,
-                              int K, long ldx, long ldo, hipStream_t stream) {
-  constexpr int RT = GEMV_WAVES / S;
-  constexpr size_t lds = gemv_lds_bytes<XI>();
-  // above 64 KB of dynamic LDS a kernel must opt in; once per instantiation and process (a
-  // function attribute, not stream work, so it is also legal under graph capture)
-  static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_bf16_kernel<S, XI>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (attr != hipSuccess) return attr;
-  const int tiles = (N + 15) / 16;
-  gemv_bf16_kernel<S, XI><<<dim3((tiles + RT - 1) / RT), dim3(GEMV_WAVES * WAVE), lds, stream>>>(
-      W, x, out, nr, N, K, ldx, ldo);
-  return hipGetLastError();
-}
-
 template <int S>
 static hipError_t launch_gemv_xr(const __bf16* W, const __bf16* x, __bf16* out, int nr, int N,
                                  int K, long ldx, long ldo, hipStream_t stream) {
@@ -299,17 +174,8 @@ static hipError_t launch_gemv_xr(const __bf16* W, const __bf16* x, __bf16* out, 
   return hipGetLastError();
 }
 
-template <int XI>
-static hipError_t launch_gemv_s(int S, const __bf16* W, const __bf16* x, __bf16* out, int nr,
-                                int N, int K, long ldx, long ldo, hipStream_t stream) {
-  switch (S) {
-    case 1: return launch_gemv<1, XI>(W, x, out, nr, N, K, ldx, ldo, stream);
-    case 2: return launch_gemv<2, XI>(W, x, out, nr, N, K, ldx, ldo, stream);
-    default: return launch_gemv<4, XI>(W, x, out, nr, N, K, ldx, ldo, stream);
-  }
-}
-
 }  // namespace qe
+
 
 using namespace qe;
 
@@ -347,12 +213,7 @@ extern "C" hipError_t qe_gemv_bf16(const void* W, const void* x, void* out, int 
       default: return launch_gemv_xr<4>(Wb, xb, ob, nr, N, K, ldx, ldo, stream);
     }
   }
-  switch ((nr + 1) / 2) {
-    case 1: return launch_gemv_s<1>(S, Wb, xb, ob, nr, N, K, ldx, ldo, stream);
-    case 2: return launch_gemv_s<2>(S, Wb, xb, ob, nr, N, K, ldx, ldo, stream);
-    case 3: return launch_gemv_s<3>(S, Wb, xb, ob, nr, N, K, ldx, ldo, stream);
-    default: return launch_gemv_s<4>(S, Wb, xb, ob, nr, N, K, ldx, ldo, stream);
-  }
+  return launch_gemv_lds(S, (nr + 1) / 2, Wb, xb, ob, nr, N, K, ldx, ldo, stream);
 }
 
 extern "C" hipError_t qe_hbm_read_probe(const void* buf, size_t bytes, void* sink,
