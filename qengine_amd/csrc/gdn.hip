@@ -13,8 +13,8 @@
 // pattern of calls with kept prefixes equals plain one-row decoding bit for bit.
 //
 // Two paths share the per-column arithmetic (gdn_common.hpp) and so give the same bits:
-// gdn_step_kernel (one workgroup per head, below) for 1-4 rows, and gdn_split_kernel (each head
-// over 4 workgroups) followed by gdn_finish_kernel (gdn_split.hip) for 5-8 rows.
+// gdn_step_kernel (one workgroup per head, below) for 1-3 rows, and gdn_split_kernel (each head
+// over 4 workgroups) followed by gdn_finish_kernel (gdn_split.hip) for 4-8 rows.
 //
 // gfx950 layout: one 512-thread workgroup (8 waves) per value head. Wave w owns state columns
 // 16w .. 16w+15; lane l holds rows 8(l>>2) .. +7 of columns 16w + 4(l&3) .. +3 (32 fp32 registers,
@@ -208,10 +208,11 @@ extern "C" hipError_t qe_gdn_step_n(const void* qkv, const void* z, const void* 
   if (C >= (1L << 26) || ldp < C || ldo < (long)Hv * GDN_D) return hipErrorInvalidValue;
   if (!al(S, 16) || !al(st_k, 16) || !al(st_v, 16) || !al(st_g, 8) || !al(conv_w, 8))
     return hipErrorInvalidValue;
-  // 5-8 rows: the split kernel and its finish kernel; 1-4 rows: one workgroup per head (below
-  // five rows the split's second launch costs more than the spread saves: same-box A/B on
-  // MI355X at Hk 16 / Hv 48, 2 rows 11.2 vs 9.5 us, 4 rows 12.9 vs 12.6, 6 rows 15.4 vs 15.7,
-  // 8 rows 17.4 vs 18.8). Both paths give the same bits.
+  // 4-8 rows: the split kernel and its finish kernel; 1-3 rows: one workgroup per head (below
+  // four rows the split's second launch costs more than the spread saves: same-box A/B on
+  // MI355X at Hk 16 / Hv 48 with the split path under the max-ILP scheduler, 3 rows 11.60 vs
+  // 10.92 us, 4 rows 12.35 vs 12.67; earlier, 6 rows 15.4 vs 15.7 and 8 rows 17.4 vs 18.8).
+  // Both paths give the same bits.
   if (n >= GDN_SPLIT_MIN_ROWS)
     return launch_gdn_split(static_cast<const __bf16*>(qkv), static_cast<const __bf16*>(z),
                             static_cast<const __bf16*>(b), static_cast<const __bf16*>(a), ldp,

@@ -17,7 +17,7 @@ constexpr int GDN_THREADS = 512;
 constexpr int GDN_SPLIT = 4;                        // workgroups per head in the split kernel
 constexpr int GDN_SPLIT_COLS = GDN_D / GDN_SPLIT;
 constexpr int GDN_SPLIT_THREADS = 512;
-constexpr int GDN_SPLIT_MIN_ROWS = 5;               // fewer rows: the one-workgroup kernel
+constexpr int GDN_SPLIT_MIN_ROWS = 4;               // fewer rows: the one-workgroup kernel
 
 struct __align__(16) F4 {
   float x, y, z, w;
@@ -128,7 +128,7 @@ __device__ __forceinline__ void gated_norm_row(const float* __restrict__ o_row, 
   op[2 * lane + 1] = f32_to_bf16(y1 * silu_f(z1));
 }
 
-// Split path for 5-8 rows (gdn_split.hip): gdn_split_kernel then gdn_finish_kernel.
+// Split path for 4-8 rows (gdn_split.hip): gdn_split_kernel then gdn_finish_kernel.
 hipError_t launch_gdn_split(const __bf16* qkv, const __bf16* z, const __bf16* b, const __bf16* a,
                             long ldp, __bf16* ring, const __bf16* conv_w, const __bf16* A_log,
                             const __bf16* dt_bias, const __bf16* norm_w, float* S, float* st_k,
