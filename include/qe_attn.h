@@ -56,7 +56,7 @@ hipError_t qe_attn_decode(const void* q, const void* kc, const void* vc, const i
  * launches instead of three: the split-KV kernel computes its q rows and writes the new K/V
  * cache rows itself, then the combine runs. Every output (q_out, the written cache rows, out) is
  * bit-identical to the two calls in sequence. Valid: the union of both ops' ranges (1 <= n <= 8,
- * (Hq/Hkv)*n <= 64, ...); shapes wider than 32 columns ((Hq/Hkv)*n > 32) run the two ops.
+ * (Hq/Hkv)*n <= 64, ...); shapes wider than 16 columns ((Hq/Hkv)*n > 16) run the two ops.
  * No counterpart in the reference, which overlaps the two launches with programmatic dependent
  * launch instead (csrc/attn.cu:155, csrc/common.cuh:12-46; callers python/qengine/engine.py:455-458). */
 hipError_t qe_attn_prep_decode(const void* qg, const void* k, const void* v, long ldp,

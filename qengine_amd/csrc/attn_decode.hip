@@ -151,6 +151,59 @@ __device__ __forceinline__ void wait_and_compute(const VTile& b, const u32x4_t* 
   }
 }
 
+// Fused prep + decode: the wave's first tile is loaded before the prep. Its K goes to registers
+// (KRegs: chunk k[j] of lane i is the one load_tile's LDS-DMA instruction j would put in slot
+// 64j + i), not to LDS by DMA: the compiler cannot tell the DMA's LDS target from the prep's LDS
+// and would make the prep's first LDS read wait for the tile.
+struct KRegs {
+  u32x4_t k[16];
+};
+__device__ __forceinline__ void load_tile_regs(KRegs& kr, VTile& b, __amdgpu_buffer_rsrc_t krs,
+                                               __amdgpu_buffer_rsrc_t vrs, int p0, int lane, int c,
+                                               int g4) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int r = 2 * j + (lane >> 5);
+    const int q = (lane & 31) ^ (r & 15);
+    kr.k[j] = buffer_load16_stream(krs, (uint32_t)(p0 + r) * (HD * 2) + q * 16);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      b.v[e][h] = buffer_load16_stream(
+          vrs, (uint32_t)(p0 + 16 * (e >> 2) + 4 * g4 + (e & 3)) * (HD * 2) + (128 * h + 8 * c) * 2);
+}
+
+// After the prep: the tile's rows at the positions the prep wrote (pos0 + t, t in [t_lo, t_hi))
+// hold stale bytes; their K rows (staged by the prep, FusedLds::knew) and V rows (vnew) replace
+// them in the registers, so the tile holds what a load after the write would have read. K then
+// goes to the wave's LDS tile.
+__device__ __forceinline__ void fused_place_tile(KRegs& kr, VTile& b, u32x4_t* ks_lds,
+                                                 const u32x4_t (*knew)[ROW_CHUNKS],
+                                                 const u32x4_t (*vnew)[ROW_CHUNKS], int p0,
+                                                 int pos0, int t_lo, int t_hi, int lane, int c,
+                                                 int g4) {
+  if (t_hi > t_lo) {  // uniform
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int r = 2 * j + (lane >> 5);
+      const int t = p0 + r - pos0;
+      if (t >= t_lo && t < t_hi) kr.k[j] = knew[t][(lane & 31) ^ (r & 15)];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int t = p0 + 16 * (e >> 2) + 4 * g4 + (e & 3) - pos0;
+      if (t >= t_lo && t < t_hi) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) b.v[e][h] = vnew[t][16 * h + c];
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) ks_lds[64 * j + lane] = kr.k[j];
+}
+
 // fp8 KV (E4M3FN codes, 256-byte rows): the same tile and the same arithmetic after an exact
 // conversion to bf16. K: 8 LDS-DMA loads (instruction j covers rows 4j..4j+3; lane i fetches the
 // 16-byte chunk that belongs in slot 64j + i, chunks XOR-swizzled by row as for bf16); V: 16
@@ -249,6 +302,7 @@ struct PrepIn {
 constexpr int FQ_ROW_U4 = ROW_CHUNKS + 1;
 constexpr int PREP_WAVES = 4;
 constexpr int ROPE_TAB = 256;  // n * rd/2 entries, one per thread (the fused path's limit)
+constexpr int FUSED_NEW_ROWS = 8;  // rows of a call (n <= 8)
 template <int NT>
 struct PrepShape {
   static constexpr int MAXI = (16 * NT + 8 + PREP_WAVES - 1) / PREP_WAVES;  // items per wave
@@ -262,8 +316,10 @@ struct FusedLds {
   float stage_f[PREP_WAVES][HD / 2];          // inv_freq (half <= 128)
   float xn[PREP_WAVES][HD];
   float cs[ROPE_TAB], sn[ROPE_TAB];
+  u32x4_t knew[FUSED_NEW_ROWS][ROW_CHUNKS];  // the cache rows this workgroup writes, by row t:
+  u32x4_t vnew[FUSED_NEW_ROWS][ROW_CHUNKS];  // patched into the tile loaded before the prep
 };
-__shared__ __attribute__((aligned(16))) char fused_lds_raw[sizeof(FusedLds<2>)];
+__shared__ __attribute__((aligned(16))) char fused_lds_raw[sizeof(FusedLds<1>)];
 template <int NT>
 __device__ __forceinline__ FusedLds<NT>& fused_lds() {
   return *reinterpret_cast<FusedLds<NT>*>(fused_lds_raw);
@@ -305,7 +361,9 @@ __device__ __forceinline__ void fused_prep_load(PrepRegs<NT>& r, const PrepIn& p
   }
   r.w = reinterpret_cast<const u32x4_t*>(hl ? pin.knw : pin.qnw)[ch];
   const int half = pin.rd >> 1;  // a multiple of 4 on this path
-  r.f = reinterpret_cast<const u32x4_t*>(pin.inv_freq)[lane < half / 4 ? lane : 0];
+  // lanes past the table load (and stage) its last chunk again, so the staging store needs no
+  // branch that the compiler could sink this load into
+  r.f = reinterpret_cast<const u32x4_t*>(pin.inv_freq)[min(lane, half / 4 - 1)];
 }
 
 template <int NT, int K>
@@ -366,29 +424,37 @@ __device__ __forceinline__ void fused_prep_item(const PrepIn& pin, int s, int g,
   } else {
     const size_t dst = ((size_t)g * max_len + (pos0 + t)) * HD;
     const __bf16* vrow = pin.v + (size_t)t * pin.ldp + (size_t)g * HD;
+    __bf16* kn = reinterpret_cast<__bf16*>(&L.knew[t][0]);
+    __bf16* vn = reinterpret_cast<__bf16*>(&L.vnew[t][0]);
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      kc[dst + lane + 64 * rr] = f32_to_bf16(y[rr]);
-      vc[dst + lane + 64 * rr] = vrow[lane + 64 * rr];  // bit for bit
+      const __bf16 kb = f32_to_bf16(y[rr]), vb = vrow[lane + 64 * rr];  // v bit for bit
+      kc[dst + lane + 64 * rr] = kb;
+      vc[dst + lane + 64 * rr] = vb;
+      kn[lane + 64 * rr] = kb;
+      vn[lane + 64 * rr] = vb;
     }
   }
 }
 
-// Ends with a workgroup barrier after which the q rows are readable in LDS and, in the workgroup
-// that writes cache rows, those writes have completed (so the waves' later tile loads see them).
-template <int NT, int... Ks>
-__device__ __forceinline__ void fused_prep_compute(const PrepRegs<NT>& r, const PrepIn& pin, int s,
-                                                   int g, int grp, int n, int Hq, int ncols,
-                                                   int pos0, int t_lo, int t_hi, int max_len,
-                                                   __bf16* kc, __bf16* vc,
-                                                   std::integer_sequence<int, Ks...>) {
+// The loaded input rows into this wave's LDS staging area (waits for the loads).
+template <int NT>
+__device__ __forceinline__ void fused_prep_stage(const PrepRegs<NT>& r, const PrepIn& pin) {
   FusedLds<NT>& L = fused_lds<NT>();
   const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
   const int hl = lane >> 5, ch = lane & 31, half = pin.rd >> 1;
 #pragma unroll
   for (int P = 0; P < PrepShape<NT>::PAIRS; ++P) L.stage_x[w][2 * P + hl][ch] = r.x[P];
   L.stage_w[w][hl][ch] = r.w;
-  if (lane < half / 4) reinterpret_cast<u32x4_t*>(L.stage_f[w])[lane] = r.f;
+  reinterpret_cast<u32x4_t*>(L.stage_f[w])[min(lane, half / 4 - 1)] = r.f;  // same bits per slot
+}
+
+// After fused_prep_stage: the rotary cos/sin table of the call's rows, then a workgroup barrier.
+template <int NT>
+__device__ __forceinline__ void fused_prep_table(const PrepIn& pin, int n, int pos0) {
+  FusedLds<NT>& L = fused_lds<NT>();
+  const int w = threadIdx.x / WAVE;
+  const int half = pin.rd >> 1;
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -399,6 +465,16 @@ __device__ __forceinline__ void fused_prep_compute(const PrepRegs<NT>& r, const 
     L.sn[e] = cs.sn;
   }
   lds_barrier();
+}
+
+// After fused_prep_table. Ends with a workgroup barrier after which the q rows are readable in
+// LDS and, in the workgroup that writes cache rows, those writes have completed (so the waves'
+// later tile loads see them).
+template <int NT, int... Ks>
+__device__ __forceinline__ void fused_prep_compute(const PrepIn& pin, int s, int g, int grp, int n,
+                                                   int Hq, int ncols, int pos0, int t_lo,
+                                                   int t_hi, int max_len, __bf16* kc, __bf16* vc,
+                                                   std::integer_sequence<int, Ks...>) {
   const int nitems = ncols + (t_hi - t_lo);
   (fused_prep_item<NT, Ks>(pin, s, g, grp, Hq, ncols, nitems, pos0, t_lo, max_len, kc, vc), ...);
   if (t_hi > t_lo)
@@ -466,18 +542,40 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
   __shared__ __attribute__((aligned(16))) char lds[lds_k_bytes<WAVES>()];
   __shared__ float s_m[WAVES][16 * NT], s_l[WAVES][16 * NT];
   static_assert(!(FUSED && KV8), "the fused prep writes a bf16 cache");
+  static_assert(!FUSED || NT == 1, "the fused prep runs at one column tile");
   u32x4_t* ks_lds = reinterpret_cast<u32x4_t*>(lds) + w * TILE * ROW_CHUNKS;
   constexpr int ELEM = KV8 ? 1 : 2;  // bytes per cache value
   const size_t head_off = (size_t)g * max_len * HD * ELEM;  // bytes
 
+  // K/V buffer resources of a pass: loads past the pass's last position read 0
+  auto pass_rsrc = [&](const Pass P, const __bf16* base) __attribute__((always_inline)) {
+    const uint32_t bytes = (uint32_t)P.end * (uint32_t)(HD * ELEM);
+    return make_rsrc_uniform(reinterpret_cast<const char*>(base) + head_off, bytes);
+  };
+  VTile buf;        // V registers of the wave's current tile
+  KRegs kpf;        // fused: K of the tile loaded before the prep
+  bool pf = false;  // fused: the first tile of the first pass was loaded before the prep
+  int t_lo = 0, t_hi = 0;
   if constexpr (FUSED) {
     // rows t in [t_lo, t_hi) sit at positions this workgroup reads: their K/V rows are written here
     const int lo = attendA ? PA.beg : PB.beg, hi = attendB ? PB.end : PA.end;
-    const int t_lo = max(lo - pos0, 0);
-    const int t_hi = attend ? max(min(hi - pos0, n), t_lo) : t_lo;  // empty when none is here
+    t_lo = max(lo - pos0, 0);
+    t_hi = attend ? max(min(hi - pos0, n), t_lo) : t_lo;  // empty when none is here
     PrepRegs<NT> pr;
     fused_prep_load<NT>(pr, pin, g, grp, n, ncols, t_lo, t_hi);
-    fused_prep_compute<NT>(pr, pin, s, g, grp, n, Hq, ncols, pos0, t_lo, t_hi, max_len,
+    fused_prep_stage<NT>(pr, pin);
+    fused_prep_table<NT>(pin, n, pos0);
+    // The wave's first tile does not depend on the prep (rows the prep writes are patched in
+    // after it, fused_patch_tile): its loads go out once the prep's inputs are staged (so no wait
+    // for those inputs can also wait for the tile) and the rotary table, which one wave computes
+    // for all, is done, and land while the items run.
+    const Pass P0 = attendA ? PA : PB;
+    const int pf_p0 = P0.beg + w * TILE;
+    pf = attend && pf_p0 < P0.end;
+    __builtin_amdgcn_sched_barrier(0);
+    if (pf) load_tile_regs(kpf, buf, pass_rsrc(P0, kc), pass_rsrc(P0, vc), pf_p0, lane, c, g4);
+    __builtin_amdgcn_sched_barrier(0);
+    fused_prep_compute<NT>(pin, s, g, grp, n, Hq, ncols, pos0, t_lo, t_hi, max_len,
                            const_cast<__bf16*>(kc), const_cast<__bf16*>(vc),
                            std::make_integer_sequence<int, PrepShape<NT>::MAXI>{});
     if (!attend) return;  // slice 0 beyond every attended position: q_out written, nothing else
@@ -493,16 +591,13 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
 
   // One pass, inlined once per call of the lambda (as a loop over passes, the merge's
   // loop-invariant addresses would be hoisted and stay live through the tile loop).
-  auto run_pass = [&](const Pass P) __attribute__((always_inline)) {
+  auto run_pass = [&](const Pass P, bool first) __attribute__((always_inline)) {
     int Lcol[NT];  // attended length of the pass's columns; 0 (all masked) for the others
 #pragma unroll
     for (int ct = 0; ct < NT; ++ct)
       Lcol[ct] = in_pass(ct * 16 + c, grp, P) ? min(pos0 + trow[ct] + 1, max_len) : 0;
-    const uint32_t bytes = (uint32_t)P.end * (uint32_t)(HD * ELEM);  // loads past the slice read 0
-    const __amdgpu_buffer_rsrc_t krs =
-        make_rsrc_uniform(reinterpret_cast<const char*>(kc) + head_off, bytes);
-    const __amdgpu_buffer_rsrc_t vrs =
-        make_rsrc_uniform(reinterpret_cast<const char*>(vc) + head_off, bytes);
+    const __amdgpu_buffer_rsrc_t krs = pass_rsrc(P, kc);
+    const __amdgpu_buffer_rsrc_t vrs = pass_rsrc(P, vc);
 
     float m[NT], l[NT];
     f32x4_t acc[NT][16];  // [8hh + i]: O^T dims 128hh + 32g4 + 8ii + i (tile::pv_half)
@@ -521,8 +616,16 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
         wait_and_compute8<NT>(buf, ks_lds, p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
       }
     } else {
-      VTile buf;
-      for (int p0 = P.beg + w * TILE; p0 < P.end; p0 += WAVES * TILE) {
+      int p0 = P.beg + w * TILE;
+      if constexpr (FUSED) {
+        if (first && pf) {  // the tile loaded before the prep
+          fused_place_tile(kpf, buf, ks_lds, fused_lds<NT>().knew, fused_lds<NT>().vnew, p0, pos0,
+                           t_lo, t_hi, lane, c, g4);
+          wait_and_compute<NT>(buf, ks_lds, p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
+          p0 += WAVES * TILE;
+        }
+      }
+      for (; p0 < P.end; p0 += WAVES * TILE) {
         load_tile(buf, ks_lds, krs, vrs, p0, lane, c, g4);
         wait_and_compute<NT>(buf, ks_lds, p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
       }
@@ -650,11 +753,11 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
       }
     }
   };
-  if (attendA) run_pass(PA);
+  if (attendA) run_pass(PA, true);
   if constexpr (MULTI) {
     if (attendB) {
       if (attendA) __syncthreads();  // the merge's LDS reads are done before the next pass
-      run_pass(PB);
+      run_pass(PB, !attendA);
     }
   }
 }
@@ -1300,9 +1403,11 @@ extern "C" hipError_t qe_attn_prep_decode(const void* qg, const void* k, const v
   if (!aligned16(q_out) || !aligned16(kc) || !aligned16(vc) || !aligned16(part_o))
     return hipErrorInvalidValue;
   const int NT = ((Hq / Hkv) * n + 15) / 16;
-  // Wide verify shapes, rotary parts with more table entries than threads or not a multiple of 8
-  // dims, and input rows the 16-byte loads cannot read: the prep kernel, then the decode.
-  if (NT > 2 || rd == 0 || rd % 8 != 0 || n * (rd / 2) > ROPE_TAB || ldp % 8 != 0 ||
+  // Shapes wider than one column tile, rotary parts with more table entries than threads or not
+  // a multiple of 8 dims, and input rows the 16-byte loads cannot read: the prep kernel, then the
+  // decode. (Two column tiles fused, 3-5 rows at GQA 6, measured slower than the two ops: 25.9
+  // against 18.9 us per layer-call at 5 rows on a 4k cache, same bits.)
+  if (NT > 1 || rd == 0 || rd % 8 != 0 || n * (rd / 2) > ROPE_TAB || ldp % 8 != 0 ||
       !aligned16(qg) || !aligned16(k) || !aligned16(qnw) || !aligned16(knw) ||
       !aligned16(inv_freq)) {
     e = qe_attn_prep(qg, k, v, ldp, qnw, knw, inv_freq, pos, q_out, kc, vc, n, Hq, Hkv, max_len,
@@ -1320,14 +1425,11 @@ extern "C" hipError_t qe_attn_prep_decode(const void* qg, const void* k, const v
   const float scale_log2 = scale * 1.4426950408889634f;
   const auto* K = static_cast<const __bf16*>(kc);
   const auto* V = static_cast<const __bf16*>(vc);
-  if (NT == 1 && n == 1)
+  if (n == 1)
     attn_partials_kernel<1, true, false><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(
         nullptr, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, pin);
-  else if (NT == 1)
-    attn_partials_kernel<1, true><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(
-        nullptr, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, pin);
   else
-    attn_partials_kernel<2, true><<<grid, dim3(waves_for<2>() * WAVE), 0, stream>>>(
+    attn_partials_kernel<1, true><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(
         nullptr, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, pin);
   e = hipGetLastError();
   if (e != hipSuccess) return e;

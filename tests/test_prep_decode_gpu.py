@@ -46,7 +46,7 @@ def _run(C, fused, kc, vc, pr, qnw, knw, inv, pos, hq, ns):
 @pytest.mark.parametrize("hq,hkv,n,pos,max_len,ns", [
     (24, 4, 1, 1023, 1024, 32),       # BASELINE cfg 1 shape: the new row is the cache's last
     (24, 4, 2, 4000, 8192, 64),       # cache longer than the attended prefix
-    (24, 4, 5, 4096, 4101, 16),       # MTP verify shape (two column tiles)
+    (24, 4, 5, 4096, 4101, 16),       # MTP verify shape (two column tiles: runs the two ops)
     (24, 4, 8, 4096, 4104, 16),       # three column tiles: runs prep + decode inside the op
     (8, 2, 3, 30, 100, 4),            # new rows straddle a slice boundary (slices of 32)
     (6, 1, 4, 62, 64, 2),             # rows past the end of the cache are not written
@@ -54,6 +54,8 @@ def _run(C, fused, kc, vc, pr, qnw, knw, inv, pos, hq, ns):
     (24, 4, 2, 131070, 131072, 64),   # long cache
     (24, 4, 2, 2047, 4096, 64),       # rows straddle a slice-size change (32 | 64): two passes
     (24, 4, 5, 2046, 2100, 64),       # the same with two column tiles
+    (24, 4, 1, 16383, 16384, 64),     # the new row in a wave's second tile (loaded after the prep)
+    (24, 4, 2, 8190, 8192, 64),       # two new rows in a tile loaded before the prep (patched)
 ])
 def test_prep_decode_equals_prep_then_decode(native, hq, hkv, n, pos, max_len, ns):
     kc, vc, pr, qnw, knw, inv = _inputs(hq, hkv, n, pos, max_len, seed=hq * 100 + n)
