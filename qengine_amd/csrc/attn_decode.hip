@@ -177,13 +177,15 @@ __device__ __forceinline__ void load_tile_regs(KRegs& kr, VTile& b, __amdgpu_buf
 
 // After the prep: the tile's rows at the positions the prep wrote (pos0 + t, t in [t_lo, t_hi))
 // hold stale bytes; their K rows (staged by the prep, FusedLds::knew) and V rows (vnew) replace
-// them in the registers, so the tile holds what a load after the write would have read. K then
-// goes to the wave's LDS tile.
+// them in the registers, so the tile holds what a load after the write would have read. Positions
+// at or past the pass's end (p_end) keep the zeros the bounded load returned, as in the unfused
+// decode. K then goes to the wave's LDS tile.
 __device__ __forceinline__ void fused_place_tile(KRegs& kr, VTile& b, u32x4_t* ks_lds,
                                                  const u32x4_t (*knew)[ROW_CHUNKS],
                                                  const u32x4_t (*vnew)[ROW_CHUNKS], int p0,
-                                                 int pos0, int t_lo, int t_hi, int lane, int c,
-                                                 int g4) {
+                                                 int p_end, int pos0, int t_lo, int t_hi,
+                                                 int lane, int c, int g4) {
+  t_hi = min(t_hi, p_end - pos0);
   if (t_hi > t_lo) {  // uniform
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
@@ -619,8 +621,8 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
       int p0 = P.beg + w * TILE;
       if constexpr (FUSED) {
         if (first && pf) {  // the tile loaded before the prep
-          fused_place_tile(kpf, buf, ks_lds, fused_lds<NT>().knew, fused_lds<NT>().vnew, p0, pos0,
-                           t_lo, t_hi, lane, c, g4);
+          fused_place_tile(kpf, buf, ks_lds, fused_lds<NT>().knew, fused_lds<NT>().vnew, p0,
+                           P.end, pos0, t_lo, t_hi, lane, c, g4);
           wait_and_compute<NT>(buf, ks_lds, p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
           p0 += WAVES * TILE;
         }
