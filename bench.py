@@ -161,6 +161,9 @@ def capture(torch, fn):
 
 MIN_WARMUP_REPLAYS = 30  # the reference's time_graph warms each graph up 30 times
 MIN_WARMUP_SECONDS = 0.1  # and at least this long per graph: clocks ramp over tens of ms
+# MFMA-bound graphs (the prefill legs) take longer to reach steady clocks: after 0.1 s of replays
+# the first timing of a prefill graph read 5-10% slow in same-process A/Bs on MI355X
+MIN_WARMUP_SECONDS_MFMA = 1.0
 
 
 class Timing:
@@ -176,13 +179,14 @@ class Timing:
         return {k: round(getattr(self, k) * 1e3 / div, 3) for k in ("median", "mean", "min", "max")}
 
 
-def time_graphs(torch, graphs, steps: int, warmup: int) -> Timing:
+def time_graphs(torch, graphs, steps: int, warmup: int,
+                min_seconds: float = MIN_WARMUP_SECONDS) -> Timing:
     """The reference's graph timing (bench/engine/micro_kernels.py:16-32): at least 30 warm-up
-    replays (and at least MIN_WARMUP_SECONDS of them), then ``steps`` timed replays (graphs
+    replays (and at least ``min_seconds`` of them), then ``steps`` timed replays (graphs
     round-robin), each bracketed by events on the current stream, the one the graphs' kernels
     run on."""
     t0, i = time.perf_counter(), 0
-    while i < max(warmup, MIN_WARMUP_REPLAYS) or time.perf_counter() - t0 < MIN_WARMUP_SECONDS:
+    while i < max(warmup, MIN_WARMUP_REPLAYS) or time.perf_counter() - t0 < min_seconds:
         for _ in range(10):
             graphs[i % len(graphs)].replay()
             i += 1
@@ -287,9 +291,10 @@ def launch_floor_us(torch, steps: int, warmup: int) -> float:
     return time_graphs(torch, [capture(torch, run)], steps, warmup).median * 1e3 / LAYERS
 
 
-def time_fn_graph(torch, fn, steps: int, warmup: int) -> float:
+def time_fn_graph(torch, fn, steps: int, warmup: int,
+                  min_seconds: float = MIN_WARMUP_SECONDS) -> float:
     """ms per replay (median) of a graph capturing fn()."""
-    return time_graphs(torch, [capture(torch, fn)], steps, warmup).median
+    return time_graphs(torch, [capture(torch, fn)], steps, warmup, min_seconds).median
 
 
 def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
@@ -625,12 +630,14 @@ def bench_prefill(torch, C, steps: int, warmup: int) -> dict:
     posT = torch.tensor([pos0], dtype=torch.int32, device=dev)
     C.attn_prep_chunk(qgT, kT, vT, qnw, knw, inv, posT, qT, kc, vc, 1e-6)
     flops = 4 * D * HQ * sum(pos0 + 1 + t for t in range(T))
-    ms_attn = time_fn_graph(torch, lambda: C.attn_prefill(qT, kc, vc, posT, qgT, outT), steps, warmup)
+    mw = MIN_WARMUP_SECONDS_MFMA
+    ms_attn = time_fn_graph(torch, lambda: C.attn_prefill(qT, kc, vc, posT, qgT, outT), steps, warmup,
+                            mw)
 
     def full():
         C.attn_prep_chunk(qgT, kT, vT, qnw, knw, inv, posT, qT, kc, vc, 1e-6)
         C.attn_prefill(qT, kc, vc, posT, qgT, outT)
-    ms_full = time_fn_graph(torch, full, steps, warmup)
+    ms_full = time_fn_graph(torch, full, steps, warmup, mw)
     tflops = flops / (ms_attn * 1e-3) / 1e12
     res["cfg5_prefill_2048_on_2048"] = {
         "us_attention": round(ms_attn * 1e3, 2), "us_prep_plus_attention": round(ms_full * 1e3, 2),
@@ -646,12 +653,12 @@ def bench_prefill(torch, C, steps: int, warmup: int) -> dict:
     vc8.copy_((vc.float() * 16).clamp(-448, 448).to(torch.float8_e4m3fn))
     C.attn_prep_fp8(qgT, kT, vT, qnw, knw, inv, posT, qT, kc8, vc8, 1e-6, ks, vs)
     ms8 = time_fn_graph(torch, lambda: C.attn_prefill_fp8(qT, kc8, vc8, posT, qgT, outT, ks, vs),
-                        steps, warmup)
+                        steps, warmup, mw)
 
     def full8():
         C.attn_prep_fp8(qgT, kT, vT, qnw, knw, inv, posT, qT, kc8, vc8, 1e-6, ks, vs)
         C.attn_prefill_fp8(qT, kc8, vc8, posT, qgT, outT, ks, vs)
-    ms8_full = time_fn_graph(torch, full8, steps, warmup)
+    ms8_full = time_fn_graph(torch, full8, steps, warmup, mw)
     tf8 = flops / (ms8 * 1e-3) / 1e12
     res["cfg5_prefill_fp8kv"] = {
         "us_attention": round(ms8 * 1e3, 2), "us_prep_plus_attention": round(ms8_full * 1e3, 2),
