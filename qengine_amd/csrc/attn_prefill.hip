@@ -105,11 +105,11 @@ __device__ __forceinline__ void run_tiles(int j0, int j1, int Lwave, u32x4_t* ld
       issue_tile(lds + ((j + AHEAD) % STAGES) * STAGE_U4, krs, vrs, p0 + AHEAD * BN, w, lane);
     if (p0 >= Lwave) continue;      // tiles past this wave's rows contribute nothing
     f32x4_t sacc[NT][2];
-    tile::qk_tile<NT>(kt, qb, c, g4, sacc);
+    tile::qk_tile<NT, NT == 1>(kt, qb, c, g4, sacc);
     u32x4_t pb_hi[NT], pb_lo[NT];
     tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc, pb_hi,
                                         pb_lo);
-    tile::pv_tile_tr<NT, SPLIT>(vt, lane, g4, pb_hi, pb_lo, st.acc);
+    tile::pv_tile_tr<NT, SPLIT, NT == 1>(vt, lane, g4, pb_hi, pb_lo, st.acc);
   }
 }
 
@@ -162,11 +162,11 @@ __device__ __forceinline__ void run_tiles8(int j0, int j1, int Lwave, u32x4_t* l
     lds_barrier();  // the bf16 tile is complete
     if (p0 >= Lwave) continue;
     f32x4_t sacc[NT][2];
-    tile::qk_tile<NT>(bf, qb, c, g4, sacc);
+    tile::qk_tile<NT, NT == 1>(bf, qb, c, g4, sacc);
     u32x4_t pb_hi[NT], pb_lo[NT];
     tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc, pb_hi,
                                         pb_lo);
-    tile::pv_tile_tr<NT, SPLIT>(bf + TILE_U4, lane, g4, pb_hi, pb_lo, st.acc);
+    tile::pv_tile_tr<NT, SPLIT, NT == 1>(bf + TILE_U4, lane, g4, pb_hi, pb_lo, st.acc);
   }
 }
 
@@ -200,7 +200,7 @@ attn_prefill_kernel(const __bf16* __restrict__ q, const void* __restrict__ kc,
   const int c = lane & 15, g4 = lane >> 4;
   const int pos0 = pos_ptr[0];
 
-  __shared__ __attribute__((aligned(16))) u32x4_t lds[STAGES * STAGE_U4];  // 128 KB
+  __shared__ __attribute__((aligned(256))) u32x4_t lds[STAGES * STAGE_U4];  // 128 KB
 
   // Q^T as the MFMA B operand: column ct*16 + c is chunk row r = blk*128 + 32w + 16ct + c.
   bf16x8_t qb[NT][8];
@@ -330,11 +330,11 @@ __device__ __forceinline__ void run_tiles_bal(int j0, int j1, int Lwave, u32x4_t
                  lane);
     if (p0 >= Lwave) continue;
     f32x4_t sacc[NT][2];
-    tile::qk_tile<NT>(kt, qb, c, g4, sacc);
+    tile::qk_tile<NT, NT == 1>(kt, qb, c, g4, sacc);
     u32x4_t pb_hi[NT], pb_lo[NT];
     tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc, pb_hi,
                                         pb_lo);
-    tile::pv_tile_tr<NT, SPLIT>(vt, lane, g4, pb_hi, pb_lo, st.acc);
+    tile::pv_tile_tr<NT, SPLIT, NT == 1>(vt, lane, g4, pb_hi, pb_lo, st.acc);
   }
 }
 
@@ -361,11 +361,11 @@ __device__ __forceinline__ void run_tiles_bal8(int j0, int j1, int Lwave, u32x4_
     if (p0 >= Lwave) continue;
     const u32x4_t* bf = bfp + (j & 1) * STAGE_U4;
     f32x4_t sacc[NT][2];
-    tile::qk_tile<NT>(bf, qb, c, g4, sacc);
+    tile::qk_tile<NT, NT == 1>(bf, qb, c, g4, sacc);
     u32x4_t pb_hi[NT], pb_lo[NT];
     tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc, pb_hi,
                                         pb_lo);
-    tile::pv_tile_tr<NT, SPLIT>(bf + TILE_U4, lane, g4, pb_hi, pb_lo, st.acc);
+    tile::pv_tile_tr<NT, SPLIT, NT == 1>(bf + TILE_U4, lane, g4, pb_hi, pb_lo, st.acc);
   }
 }
 
@@ -394,7 +394,7 @@ attn_prefill_bal_kernel(const __bf16* __restrict__ q, const void* __restrict__ k
   const bool wave_live = !(half && bh == bl);  // odd block count: the middle pair has one block
   const int pos0 = pos_ptr[0];
 
-  __shared__ __attribute__((aligned(16))) u32x4_t lds[STAGES * STAGE_U4];  // 128 KB
+  __shared__ __attribute__((aligned(256))) u32x4_t lds[STAGES * STAGE_U4];  // 128 KB
 
   bf16x8_t qb[NT][8];
   int Lcol[NT];

@@ -33,23 +33,30 @@ __device__ __forceinline__ int k_slot(int r, int q) { return r * ROW_CHUNKS + (q
 // per-lane bases: one address add per base and tile, the rest immediate offsets (about 25 fewer
 // VALU instructions per tile). Callers with two or more column tiles per wave sit at the register
 // limit and keep the per-read slot arithmetic, which needs no extra live registers.
-template <int NT>
+// XA (NT == 1; the K tile 256-byte aligned in LDS): the four bases are one per-lane base XORed
+// with 64 (ks & 3), since 64 (l ^ (c >> 2)) = 64 l ^ 64 (c >> 2) touches address bits 6-7 only:
+// the same addresses, formed per tile instead of living across the caller's loop.
+template <int NT, bool XA = false>
 __device__ __forceinline__ void qk_tile(const u32x4_t* k_lds, const bf16x8_t (&qb)[NT][8], int c,
                                         int g4, f32x4_t (&sacc)[NT][2]) {
+  typedef __attribute__((address_space(3))) const u32x4_t lds_u32x4;
   const char* kb = reinterpret_cast<const char*>(k_lds);
   const char* kl[4];
 #pragma unroll
   for (int l = 0; l < 4; ++l)
     kl[l] = kb + c * (ROW_CHUNKS * 16) + 64 * (l ^ (c >> 2)) + 16 * (g4 ^ (c & 3));
+  const uint32_t k0 = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const char*)kb) +
+                      c * (ROW_CHUNKS * 16) + 64 * (c >> 2) + 16 * (g4 ^ (c & 3));
 #pragma unroll
   for (int T = 0; T < 2; ++T) {
 #pragma unroll
     for (int ct = 0; ct < NT; ++ct) sacc[ct][T] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
+      const int off = 256 * (ks >> 2) + 16 * ROW_CHUNKS * 16 * T;
       const bf16x8_t kop =
-          NT == 1 ? as_bf16x8(*reinterpret_cast<const u32x4_t*>(kl[ks & 3] + 256 * (ks >> 2) +
-                                                                 16 * ROW_CHUNKS * 16 * T))
+          NT == 1 ? (XA ? as_bf16x8(*(lds_u32x4*)(uintptr_t)((k0 ^ (64u * (ks & 3))) + off))
+                        : as_bf16x8(*reinterpret_cast<const u32x4_t*>(kl[ks & 3] + off)))
                   : as_bf16x8(k_lds[k_slot(16 * T + c, 4 * ks + g4)]);
 #pragma unroll
       for (int ct = 0; ct < NT; ++ct) sacc[ct][T] = mfma16x16x32(kop, qb[ct][ks], sacc[ct][T]);
@@ -151,7 +158,10 @@ __device__ __forceinline__ int v_swz(int r) { return 2 * (r & 7); }
 // 16-lane group element b of the 8 bytes addressed by lane a + 4e of the group, as element e
 // (lane layout checked on MI355X). So lane (a = lane & 3, lane/4 & 3, g4) addresses V row
 // 4g4 + (lane/4 & 3) (+16 for elements 4..7) at dims 16i + 4a .. +3.
-template <int NT, bool SPLIT>
+// XA (NT == 1; the V tile 256-byte aligned in LDS): the eight bases are one per-lane base XORed
+// with 32 (i & 7) (32 (l ^ (r & 7)) = 32 l ^ 32 (r & 7) touches address bits 5-7 only), formed
+// per tile instead of living across the caller's loop: 13 fewer registers in the prefill kernel.
+template <int NT, bool SPLIT, bool XA = false>
 __device__ __forceinline__ void pv_tile_tr(const u32x4_t* vt, int lane, int g4,
                                            const u32x4_t (&pb_hi)[NT], const u32x4_t (&pb_lo)[NT],
                                            f32x4_t (&acc)[NT][16]) {
@@ -166,14 +176,18 @@ __device__ __forceinline__ void pv_tile_tr(const u32x4_t* vt, int lane, int g4,
   char* vl[8];
 #pragma unroll
   for (int l = 0; l < 8; ++l) vl[l] = vr + 16 * (a >> 1) + 32 * (l ^ (r & 7));
+  const uint32_t v0 = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)vr) +
+                      16 * (a >> 1) + 32 * (r & 7);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    char* p = NT == 1 ? vl[i & 7] + 256 * (i >> 3)  // rows r and r + 16 share the swizzle
-                      : vr + ((2 * i + (a >> 1)) ^ v_swz(r)) * 16;
-    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        reinterpret_cast<lds_v4i16*>((__attribute__((address_space(3))) char*)p));
-    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        reinterpret_cast<lds_v4i16*>((__attribute__((address_space(3))) char*)(p + 16 * HD * 2)));
+    typedef __attribute__((address_space(3))) char lds_char;
+    lds_char* p =
+        NT == 1 ? (XA ? (lds_char*)(uintptr_t)((v0 ^ (32u * (i & 7))) + 256 * (i >> 3))
+                      : (lds_char*)(vl[i & 7] + 256 * (i >> 3)))  // rows r, r + 16: one swizzle
+                : (lds_char*)(vr + ((2 * i + (a >> 1)) ^ v_swz(r)) * 16);
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_v4i16*>(p));
+    const v4i16 hi =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_v4i16*>(p + 16 * HD * 2));
     const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
     const u32x4_t av = {l2[0], l2[1], h2[0], h2[1]};
 #pragma unroll
