@@ -135,7 +135,7 @@ __device__ __forceinline__ void wait_and_compute(const VTile& b, const u32x4_t* 
   vmcnt_wait<16>();
   wave_lds_fence();
   f32x4_t sacc[NT][2];
-  tile::qk_tile<NT>(ks_lds, qb, c, g4, sacc);
+  tile::qk_tile<NT, NT == 1>(ks_lds, qb, c, g4, sacc);  // (K tiles 256-byte aligned)
   wave_lds_fence();  // this tile's K reads happen before the next tile's LDS-DMA writes
   u32x4_t pb_hi[NT], pb_lo[NT];
   if (p0 + TILE > Lmin)
@@ -541,7 +541,7 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
   const bool attend = attendA || attendB;  // uniform per workgroup
   if (!attend && !(FUSED && s == 0)) return;  // (slice 0 of the fused kernel still writes q_out)
 
-  __shared__ __attribute__((aligned(16))) char lds[lds_k_bytes<WAVES>()];
+  __shared__ __attribute__((aligned(256))) char lds[lds_k_bytes<WAVES>()];  // 16 KB per wave
   __shared__ float s_m[WAVES][16 * NT], s_l[WAVES][16 * NT];
   static_assert(!(FUSED && KV8), "the fused prep writes a bf16 cache");
   static_assert(!FUSED || NT == 1, "the fused prep runs at one column tile");
