@@ -233,20 +233,22 @@ __device__ __forceinline__ void load_tile8(VTile8& b, u32x4_t* ks_lds, __amdgpu_
 
 // S^T = K Q^T from an fp8 K tile in LDS: lane (c, g4) reads the 8 codes of row 16T + c, dims
 // [32ks + 8g4, +8) (half of the swizzled 16-byte chunk 2ks + g4/2) and converts them to the bf16
-// A operand of qk_tile.
+// A operand of qk_tile. With the tile 256-byte aligned, chunk (2ks + g4/2) ^ c at byte 16 chunk
+// is one per-lane base XORed with 32 ks (the swizzle moves bits 5-7 only) plus 4096 T.
 template <int NT>
 __device__ __forceinline__ void qk_tile8(const u32x4_t* k_lds, const bf16x8_t (&qb)[NT][8], int c,
                                          int g4, f32x4_t (&sacc)[NT][2]) {
-  const char* base = reinterpret_cast<const char*>(k_lds);
+  typedef __attribute__((address_space(3))) const u32x2_t lds_u32x2;
+  const uint32_t b0 =
+      (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const char*)reinterpret_cast<const char*>(k_lds)) +
+      c * 256 + 16 * (c & 14) + 16 * ((g4 >> 1) ^ (c & 1)) + 8 * (g4 & 1);
 #pragma unroll
   for (int T = 0; T < 2; ++T) {
 #pragma unroll
     for (int ct = 0; ct < NT; ++ct) sacc[ct][T] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const int r = 16 * T + c;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-      const int chunk = (2 * ks + (g4 >> 1)) ^ (r & 15);
-      const u32x2_t w = *reinterpret_cast<const u32x2_t*>(base + (r * 16 + chunk) * 16 + (g4 & 1) * 8);
+      const u32x2_t w = *(lds_u32x2*)(uintptr_t)((b0 ^ (32u * ks)) + 4096 * T);
       const bf16x8_t kop = as_bf16x8(fp8x8_to_bf16x8(w));
 #pragma unroll
       for (int ct = 0; ct < NT; ++ct) sacc[ct][T] = mfma16x16x32(kop, qb[ct][ks], sacc[ct][T]);
