@@ -96,24 +96,43 @@ struct VTile {
   u32x4_t v[8][2];  // V rows P(g4, e) = p0 + 16(e>>2) + 4g4 + (e&3), dims 128h + 8c + [0, 8)
 };
 
-// Issue one tile's loads: 16 LDS-DMA loads of K (instruction j covers rows 2j, 2j+1: lane i
-// fetches the chunk that belongs in LDS slot 64j + i, so each instruction reads 1 KB of
-// contiguous cache), then 16 register loads of V (4 rows x 256 B per instruction).
-__device__ __forceinline__ void load_tile(VTile& b, u32x4_t* ks_lds, __amdgpu_buffer_rsrc_t krs,
-                                          __amdgpu_buffer_rsrc_t vrs, int p0, int lane, int c,
-                                          int g4) {
+// Buffer resource of one tile: based at row p0 of a head's cache (row_bytes per row), ending at
+// row p_end, so loads at rows >= p_end read 0, exactly as a resource over the whole pass would.
+// Every load's offset is then a loop-invariant lane term plus an immediate, and the per-tile
+// address arithmetic is scalar (p0 is wave-uniform).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const char* head_base, int p0,
+                                                            int p_end, uint32_t row_bytes) {
+  return make_rsrc_uniform(head_base + (size_t)p0 * row_bytes, (uint32_t)(p_end - p0) * row_bytes);
+}
+
+// Lane terms of load_tile's offsets. K instruction j covers rows 2j, 2j+1 (lane i fetches the
+// chunk that belongs in LDS slot 64j + i): row r = 2j + (i>>5), chunk (i&31) ^ (r&15), i.e. byte
+// 1024j + (kl ^ 32(j&7)) with kl = 512(i>>5) + 16((i&31) ^ (i>>5)) (the swizzle moves bits 5-7
+// only). V register e, h: row 16(e>>2) + 4g4 + (e&3), dims 128h + 8c: byte
+// vl + 8192(e>>2) + 512(e&3) + 256h with vl = 2048g4 + 16c.
+struct TileLanes {
+  uint32_t kl, vl;
+  __device__ __forceinline__ explicit TileLanes(int lane)
+      : kl(512u * (lane >> 5) + 16u * ((lane & 31) ^ (lane >> 5))),
+        vl(2048u * (lane >> 4) + 16u * (lane & 15)) {}
+};
+
+// Issue one tile's loads: 16 LDS-DMA loads of K (each reads 1 KB of contiguous cache into the
+// wave's K tile at LDS byte ks_s), then 16 register loads of V (4 rows x 256 B per instruction).
+// krs / vrs are the tile's resources (tile_rsrc). The scheduling barrier keeps every K load ahead
+// of every V load: wait_and_compute's vmcnt wait counts on that order, which nothing else gives
+// (the loads are independent, and the scheduler has interleaved them).
+__device__ __forceinline__ void load_tile(VTile& b, uint32_t ks_s, __amdgpu_buffer_rsrc_t krs,
+                                          __amdgpu_buffer_rsrc_t vrs, const TileLanes& tl) {
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int r = 2 * j + (lane >> 5);
-    const int q = (lane & 31) ^ (r & 15);
-    buffer_load16_to_lds(krs, (uint32_t)(p0 + r) * (HD * 2) + q * 16, ks_lds + 64 * j);
-  }
+  for (int j = 0; j < 16; ++j)
+    buffer_load16_to_lds_at(krs, (tl.kl ^ (32u * (j & 7))) + 1024u * j, ks_s + 1024u * j);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int e = 0; e < 8; ++e)
 #pragma unroll
     for (int h = 0; h < 2; ++h)
-      b.v[e][h] = buffer_load16_stream(
-          vrs, (uint32_t)(p0 + 16 * (e >> 2) + 4 * g4 + (e & 3)) * (HD * 2) + (128 * h + 8 * c) * 2);
+      b.v[e][h] = buffer_load16_stream(vrs, tl.vl + 8192u * (e >> 2) + 512u * (e & 3) + 256u * h);
 }
 
 // Order this wave's LDS accesses: the compiler must not move LDS reads/writes across it (lanes
@@ -214,21 +233,28 @@ struct VTile8 {
   u32x2_t v[8][2];  // V rows P(g4, e), dims 128h + 8c + [0, 8), as fp8 codes
 };
 
-__device__ __forceinline__ void load_tile8(VTile8& b, u32x4_t* ks_lds, __amdgpu_buffer_rsrc_t krs,
-                                           __amdgpu_buffer_rsrc_t vrs, int p0, int lane, int c,
-                                           int g4) {
+// Lane terms of load_tile8's offsets (tile resources as for bf16). K instruction j: row
+// r = 4j + (i>>4), chunk (i&15) ^ (r&15), i.e. byte 1024j + (kl ^ 64(j&3)) with
+// kl = 256(i>>4) + 16((i&15) ^ (i>>4)). V register e, h: byte vl + 4096(e>>2) + 256(e&3) + 128h
+// with vl = 1024g4 + 8c.
+struct TileLanes8 {
+  uint32_t kl, vl;
+  __device__ __forceinline__ explicit TileLanes8(int lane)
+      : kl(256u * (lane >> 4) + 16u * ((lane & 15) ^ (lane >> 4))),
+        vl(1024u * (lane >> 4) + 8u * (lane & 15)) {}
+};
+
+__device__ __forceinline__ void load_tile8(VTile8& b, uint32_t ks_s, __amdgpu_buffer_rsrc_t krs,
+                                           __amdgpu_buffer_rsrc_t vrs, const TileLanes8& tl) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int r = 4 * j + (lane >> 4);
-    const int q = (lane & 15) ^ (r & 15);
-    buffer_load16_to_lds(krs, (uint32_t)(p0 + r) * HD + q * 16, ks_lds + 64 * j);
-  }
+  for (int j = 0; j < 8; ++j)
+    buffer_load16_to_lds_at(krs, (tl.kl ^ (64u * (j & 3))) + 1024u * j, ks_s + 1024u * j);
+  __builtin_amdgcn_sched_barrier(0);  // K before V, as in load_tile
 #pragma unroll
   for (int e = 0; e < 8; ++e)
 #pragma unroll
     for (int h = 0; h < 2; ++h)
-      b.v[e][h] = buffer_load8_stream(
-          vrs, (uint32_t)(p0 + 16 * (e >> 2) + 4 * g4 + (e & 3)) * HD + 128 * h + 8 * c);
+      b.v[e][h] = buffer_load8_stream(vrs, tl.vl + 4096u * (e >> 2) + 256u * (e & 3) + 128u * h);
 }
 
 // S^T = K Q^T from an fp8 K tile in LDS: lane (c, g4) reads the 8 codes of row 16T + c, dims
@@ -508,7 +534,10 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
   const int pos0 = pos_ptr[0];  // first: the slicing waits for it
   const int s = blockIdx.x, g = blockIdx.y;
   const int grp = Hq / Hkv;
-  const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+  // The wave index as a wave-uniform value, so that tile positions and the addresses derived
+  // from them stay in scalar registers and the tile loop is a scalar loop.
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   const int c = lane & 15, g4 = lane >> 4;
   const int ncols = grp * n;
 
@@ -550,6 +579,9 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
   u32x4_t* ks_lds = reinterpret_cast<u32x4_t*>(lds) + w * TILE * ROW_CHUNKS;
   constexpr int ELEM = KV8 ? 1 : 2;  // bytes per cache value
   const size_t head_off = (size_t)g * max_len * HD * ELEM;  // bytes
+  const char* kbase = reinterpret_cast<const char*>(kc) + head_off;  // this KV head's K rows
+  const char* vbase = reinterpret_cast<const char*>(vc) + head_off;
+  const uint32_t ks_s = lds_byte_uniform(ks_lds);  // the wave's K tile in LDS
 
   // K/V buffer resources of a pass: loads past the pass's last position read 0
   auto pass_rsrc = [&](const Pass P, const __bf16* base) __attribute__((always_inline)) {
@@ -600,8 +632,6 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
 #pragma unroll
     for (int ct = 0; ct < NT; ++ct)
       Lcol[ct] = in_pass(ct * 16 + c, grp, P) ? min(pos0 + trow[ct] + 1, max_len) : 0;
-    const __amdgpu_buffer_rsrc_t krs = pass_rsrc(P, kc);
-    const __amdgpu_buffer_rsrc_t vrs = pass_rsrc(P, vc);
 
     float m[NT], l[NT];
     f32x4_t acc[NT][16];  // [8hh + i]: O^T dims 128hh + 32g4 + 8ii + i (tile::pv_half)
@@ -615,8 +645,9 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
 
     if constexpr (KV8) {
       VTile8 buf;
+      const TileLanes8 tl(lane);
       for (int p0 = P.beg + w * TILE; p0 < P.end; p0 += WAVES * TILE) {
-        load_tile8(buf, ks_lds, krs, vrs, p0, lane, c, g4);
+        load_tile8(buf, ks_s, tile_rsrc(kbase, p0, P.end, HD), tile_rsrc(vbase, p0, P.end, HD), tl);
         wait_and_compute8<NT>(buf, ks_lds, p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
       }
     } else {
@@ -629,8 +660,10 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
           p0 += WAVES * TILE;
         }
       }
+      const TileLanes tl(lane);
       for (; p0 < P.end; p0 += WAVES * TILE) {
-        load_tile(buf, ks_lds, krs, vrs, p0, lane, c, g4);
+        load_tile(buf, ks_s, tile_rsrc(kbase, p0, P.end, HD * 2),
+                  tile_rsrc(vbase, p0, P.end, HD * 2), tl);
         wait_and_compute<NT>(buf, ks_lds, p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
       }
     }

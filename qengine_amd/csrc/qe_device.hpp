@@ -231,6 +231,20 @@ __device__ __forceinline__ void buffer_load16_to_lds(__amdgpu_buffer_rsrc_t r, u
   __builtin_amdgcn_raw_ptr_buffer_load_lds(
       r, (__attribute__((address_space(3))) void*)lds_base, 16, (int)byte_off, 0, 0, CPOL);
 }
+// The same with the LDS destination as a byte address held in scalar registers (M0 is then set
+// by scalar moves, not a readfirstlane per load).
+__device__ __forceinline__ void buffer_load16_to_lds_at(__amdgpu_buffer_rsrc_t r,
+                                                        uint32_t byte_off, uint32_t lds_byte) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void*)(uintptr_t)lds_byte, 16, (int)byte_off, 0, 0,
+      CPOL_NT);
+}
+// LDS byte address of an LDS pointer, made wave-uniform (readfirstlane) so the compiler keeps
+// it, and the addresses derived from it, in scalar registers.
+__device__ __forceinline__ uint32_t lds_byte_uniform(const void* p) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane(
+      (int)(uint32_t)(uintptr_t)((__attribute__((address_space(3))) const char*)p));
+}
 
 // s_waitcnt vmcnt(N): at most N vector-memory loads of this wave still outstanding (gfx9
 // encoding: vmcnt low bits [3:0], high bits [15:14]; expcnt and lgkmcnt left at their maxima).
