@@ -128,7 +128,7 @@ class LayerSet8(LayerSet):
 
 def bench_length_fp8(torch, C, qa, L: int, steps: int, warmup: int) -> dict:
     """fp8 KV decode at KV length L: layer-call and partials-only µs; bytes = 2048*L (+ q)."""
-    ns = qa.default_splits(L, HKV)
+    ns = qa.default_splits(L, HKV, kv8=True)
     nsets = max(1, math.ceil(ROTATE_BYTES / (LAYERS * L * 2048)))
     gen = torch.Generator(device="cuda").manual_seed(L + 8)
     sets = [LayerSet8(torch, C, L, ns, gen) for _ in range(nsets)]
@@ -385,10 +385,10 @@ def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
         L, n, nl = P + 8, 8, 16
         q8, qg8 = rnd(n, HQ * D), rnd(n, HQ * 2 * D)
         out8 = torch.empty(n, HQ * D, dtype=BF, device=dev)
-        ns = qa.default_splits(L, HKV)
-        po8, pml8 = qa.alloc_partials(n, HQ, ns, dev)
         pos8 = torch.tensor([P], dtype=torch.int32, device=dev)
         for fp8 in (False, True):
+            ns = qa.default_splits(L, HKV, kv8=fp8)
+            po8, pml8 = qa.alloc_partials(n, HQ, ns, dev)
             kcs = [codes(L) if fp8 else rnd(HKV, L, D) for _ in range(nl)]
             vcs = [codes(L) if fp8 else rnd(HKV, L, D) for _ in range(nl)]
 

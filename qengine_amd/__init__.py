@@ -63,15 +63,21 @@ def compute_units(device=None) -> int:
         return 256
 
 
-def default_splits(max_len: int, hkv: int = 4, cus: int | None = None) -> int:
-    """Split count NS (part_o.size(2)) for a cache of ``max_len`` positions: one workgroup per
-    compute unit when the whole cache is attended (NS * Hkv = CUs), never slices shorter than
-    32 positions. Measured on MI355X, this is the fastest choice from 4k to 128k positions:
-    fewer slices leave CUs idle, more slices cost a second round of workgroups and more partials.
+def default_splits(max_len: int, hkv: int = 4, cus: int | None = None, kv8: bool = False) -> int:
+    """Split count NS (part_o.size(2)) for a cache of ``max_len`` positions: workgroups for three
+    quarters of the compute units when the whole cache is attended (NS * Hkv = 3/4 CUs, 48 at
+    Hkv 4 on 256 CUs), never slices shorter than 32 positions. Measured on MI355X (one row, 24 Q
+    / 4 KV heads, µs per layer-call at 4k / 16k / 32k / 128k): NS 48 9.52 / 16.37 / 26.02 / 81.9,
+    NS 64 (one workgroup per CU) 9.78 / 16.54 / 26.41 / 84.4; 40, 44, 52 and 56 lie between or
+    above. Longer slices spread each workgroup's tail (last tile, merge, stores) over more
+    streamed bytes; more slices cost a second round of workgroups and more partials.
+    An fp8 cache (``kv8``) streams half the bytes per slice and keeps one workgroup per CU
+    (NS 64: 12.10 / 16.82 µs at 16k / 32k against 12.44 / 17.48 at NS 48).
     NS is fixed when the scratch is allocated, so graphs stay static; a row attending L
     positions uses slices of split_size(L, NS), so about NS slices hold work at every length."""
     cus = cus or compute_units()
-    return max(1, min(math.ceil(max_len / MIN_SLICE), max(1, cus // hkv)))
+    per_head = cus // hkv if kv8 else (3 * cus) // (4 * hkv)
+    return max(1, min(math.ceil(max_len / MIN_SLICE), max(1, per_head)))
 
 
 def alloc_partials(n_rows: int, hq: int, ns: int, device="cuda"):
