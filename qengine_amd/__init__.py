@@ -64,19 +64,19 @@ def compute_units(device=None) -> int:
 
 
 def default_splits(max_len: int, hkv: int = 4, cus: int | None = None, kv8: bool = False) -> int:
-    """Split count NS (part_o.size(2)) for a cache of ``max_len`` positions: workgroups for three
-    quarters of the compute units when the whole cache is attended (NS * Hkv = 3/4 CUs, 48 at
-    Hkv 4 on 256 CUs), never slices shorter than 32 positions. Measured on MI355X (one row, 24 Q
-    / 4 KV heads, µs per layer-call at 4k / 16k / 32k / 128k): NS 48 9.52 / 16.37 / 26.02 / 81.9,
-    NS 64 (one workgroup per CU) 9.78 / 16.54 / 26.41 / 84.4; 40, 44, 52 and 56 lie between or
-    above. Longer slices spread each workgroup's tail (last tile, merge, stores) over more
-    streamed bytes; more slices cost a second round of workgroups and more partials.
-    An fp8 cache (``kv8``) streams half the bytes per slice and keeps one workgroup per CU
-    (NS 64: 12.10 / 16.82 µs at 16k / 32k against 12.44 / 17.48 at NS 48).
-    NS is fixed when the scratch is allocated, so graphs stay static; a row attending L
+    """Split count NS (part_o.size(2)) for a cache of ``max_len`` positions: 13/16 of the compute
+    units in workgroups when the whole cache is attended (NS * Hkv = 13/16 CUs, 52 at Hkv 4 on 256
+    CUs), never slices shorter than 32 positions. Measured on MI355X with the look-ahead tile loop
+    (one row, 24 Q / 4 KV heads, partials µs at 4k / 16k / 32k / 128k): NS 52 6.97 / 13.48 / 23.08
+    / 79.8; NS 48 6.98 / 13.91 / 23.49 / 80.3; NS 64 7.08 / 13.94 / 24.18 / 83.8; 40, 44, 56 and
+    60 lie between or above. The workgroups' fixed tail (last tile, merge, stores) is spread over
+    longer slices than at one workgroup per CU; more slices cost a second round of workgroups and
+    more partials. An fp8 cache (``kv8``) streams half the bytes per slice and keeps one workgroup
+    per CU (NS 64: 9.34 / 14.36 µs at 16k / 32k against 9.52 / 14.23 at NS 52, 9.55 / 15.08 at
+    NS 48). NS is fixed when the scratch is allocated, so graphs stay static; a row attending L
     positions uses slices of split_size(L, NS), so about NS slices hold work at every length."""
     cus = cus or compute_units()
-    per_head = cus // hkv if kv8 else (3 * cus) // (4 * hkv)
+    per_head = cus // hkv if kv8 else (13 * cus) // (16 * hkv)
     return max(1, min(math.ceil(max_len / MIN_SLICE), max(1, per_head)))
 
 

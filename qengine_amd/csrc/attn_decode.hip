@@ -100,9 +100,11 @@ struct VTile {
 // row p_end, so loads at rows >= p_end read 0, exactly as a resource over the whole pass would.
 // Every load's offset is then a loop-invariant lane term plus an immediate, and the per-tile
 // address arithmetic is scalar (p0 is wave-uniform).
+// A tile at or past p_end gets an empty resource: its loads read 0 and touch no memory.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const char* head_base, int p0,
                                                             int p_end, uint32_t row_bytes) {
-  return make_rsrc_uniform(head_base + (size_t)p0 * row_bytes, (uint32_t)(p_end - p0) * row_bytes);
+  return make_rsrc_uniform(head_base + (size_t)p0 * row_bytes,
+                           (uint32_t)max(p_end - p0, 0) * row_bytes);
 }
 
 // Lane terms of load_tile's offsets. K instruction j covers rows 2j, 2j+1 (lane i fetches the
@@ -135,6 +137,28 @@ __device__ __forceinline__ void load_tile(VTile& b, uint32_t ks_s, __amdgpu_buff
       b.v[e][h] = buffer_load16_stream(vrs, tl.vl + 8192u * (e >> 2) + 512u * (e & 3) + 256u * h);
 }
 
+// The two halves of load_tile for the look-ahead loop (run_pass): K of a tile into one of the
+// wave's two LDS K slots, and V of a tile into registers.
+// The lane terms pass through an empty asm so that they are formed at each issue: otherwise the
+// compiler hoists all 16 + 16 offsets out of the tile loop and keeps them live (28 more registers).
+__device__ __forceinline__ void issue_k(uint32_t ks_s, __amdgpu_buffer_rsrc_t krs,
+                                        const TileLanes& tl) {
+  uint32_t kl = tl.kl;
+  asm volatile("" : "+v"(kl));
+#pragma unroll
+  for (int j = 0; j < 16; ++j)
+    buffer_load16_to_lds_at(krs, (kl ^ (32u * (j & 7))) + 1024u * j, ks_s + 1024u * j);
+}
+__device__ __forceinline__ void issue_v(VTile& b, __amdgpu_buffer_rsrc_t vrs, const TileLanes& tl) {
+  uint32_t vl = tl.vl;
+  asm volatile("" : "+v"(vl));  // two bases (vl, vl + 8192) and immediate offsets
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      b.v[e][h] = buffer_load16_stream(vrs, vl + 8192u * (e >> 2) + 512u * (e & 3) + 256u * h);
+}
+
 // Order this wave's LDS accesses: the compiler must not move LDS reads/writes across it (lanes
 // exchange data through LDS, which single-thread alias analysis cannot see).
 __device__ __forceinline__ void wave_lds_fence() {
@@ -142,16 +166,15 @@ __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_wave_barrier();
 }
 
-// Wait for the tile's K (its 16 LDS-DMA loads were issued before the 16 V loads, so at most 16
-// loads may remain in flight), then compute the tile. Masking is needed only on tiles reaching
-// past the shortest attended length among the real columns (Lmin).
+// Compute one tile whose K has landed in the wave's LDS slot ks_lds and whose V registers are
+// loaded (the compiler waits for those). Masking is needed only on tiles reaching past the
+// shortest attended length among the real columns (Lmin).
 template <int NT>
-__device__ __forceinline__ void wait_and_compute(const VTile& b, const u32x4_t* ks_lds, int p0,
-                                                 int Lmin, const int (&Lcol)[NT],
-                                                 const bf16x8_t (&qb)[NT][8], float scale_log2,
-                                                 int c, int g4, float (&m)[NT], float (&l)[NT],
-                                                 f32x4_t (&acc)[NT][16]) {
-  vmcnt_wait<16>();
+__device__ __forceinline__ void compute_tile(const VTile& b, const u32x4_t* ks_lds, int p0,
+                                             int Lmin, const int (&Lcol)[NT],
+                                             const bf16x8_t (&qb)[NT][8], float scale_log2,
+                                             int c, int g4, float (&m)[NT], float (&l)[NT],
+                                             f32x4_t (&acc)[NT][16]) {
   wave_lds_fence();
   f32x4_t sacc[NT][2];
   tile::qk_tile<NT, NT == 1>(ks_lds, qb, c, g4, sacc);  // (K tiles 256-byte aligned)
@@ -168,6 +191,18 @@ __device__ __forceinline__ void wait_and_compute(const VTile& b, const u32x4_t* 
     for (int e = 0; e < 8; ++e) vr[e] = b.v[e][hh];
     tile::pv_half<NT, true>(vr, hh, pb_hi, pb_lo, acc);
   }
+}
+
+// Wait for the tile's K (its 16 LDS-DMA loads were issued before the 16 V loads, so at most 16
+// loads may remain in flight), then compute the tile.
+template <int NT>
+__device__ __forceinline__ void wait_and_compute(const VTile& b, const u32x4_t* ks_lds, int p0,
+                                                 int Lmin, const int (&Lcol)[NT],
+                                                 const bf16x8_t (&qb)[NT][8], float scale_log2,
+                                                 int c, int g4, float (&m)[NT], float (&l)[NT],
+                                                 f32x4_t (&acc)[NT][16]) {
+  vmcnt_wait<16>();
+  compute_tile<NT>(b, ks_lds, p0, Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
 }
 
 // Fused prep + decode: the wave's first tile is loaded before the prep. Its K goes to registers
@@ -233,7 +268,7 @@ struct VTile8 {
   u32x2_t v[8][2];  // V rows P(g4, e), dims 128h + 8c + [0, 8), as fp8 codes
 };
 
-// Lane terms of load_tile8's offsets (tile resources as for bf16). K instruction j: row
+// Lane terms of the fp8 tile loads' offsets (tile resources as for bf16). K instruction j: row
 // r = 4j + (i>>4), chunk (i&15) ^ (r&15), i.e. byte 1024j + (kl ^ 64(j&3)) with
 // kl = 256(i>>4) + 16((i&15) ^ (i>>4)). V register e, h: byte vl + 4096(e>>2) + 256(e&3) + 128h
 // with vl = 1024g4 + 8c.
@@ -243,19 +278,6 @@ struct TileLanes8 {
       : kl(256u * (lane >> 4) + 16u * ((lane & 15) ^ (lane >> 4))),
         vl(1024u * (lane >> 4) + 8u * (lane & 15)) {}
 };
-
-__device__ __forceinline__ void load_tile8(VTile8& b, uint32_t ks_s, __amdgpu_buffer_rsrc_t krs,
-                                           __amdgpu_buffer_rsrc_t vrs, const TileLanes8& tl) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-    buffer_load16_to_lds_at(krs, (tl.kl ^ (64u * (j & 3))) + 1024u * j, ks_s + 1024u * j);
-  __builtin_amdgcn_sched_barrier(0);  // K before V, as in load_tile
-#pragma unroll
-  for (int e = 0; e < 8; ++e)
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      b.v[e][h] = buffer_load8_stream(vrs, tl.vl + 4096u * (e >> 2) + 256u * (e & 3) + 128u * h);
-}
 
 // S^T = K Q^T from an fp8 K tile in LDS: lane (c, g4) reads the 8 codes of row 16T + c, dims
 // [32ks + 8g4, +8) (half of the swizzled 16-byte chunk 2ks + g4/2) and converts them to the bf16
@@ -282,13 +304,34 @@ __device__ __forceinline__ void qk_tile8(const u32x4_t* k_lds, const bf16x8_t (&
   }
 }
 
+// One fp8 tile's loads for the look-ahead loop: the K codes (8 KB) into one of the wave's two LDS
+// K slots (8 LDS-DMA loads), and the V codes into registers (16 loads of 8 bytes).
+__device__ __forceinline__ void issue_k8(uint32_t ks_s, __amdgpu_buffer_rsrc_t krs,
+                                         const TileLanes8& tl) {
+  uint32_t kl = tl.kl;
+  asm volatile("" : "+v"(kl));
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    buffer_load16_to_lds_at(krs, (kl ^ (64u * (j & 3))) + 1024u * j, ks_s + 1024u * j);
+}
+__device__ __forceinline__ void issue_v8(VTile8& b, __amdgpu_buffer_rsrc_t vrs,
+                                         const TileLanes8& tl) {
+  uint32_t vl = tl.vl;
+  asm volatile("" : "+v"(vl));
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      b.v[e][h] = buffer_load8_stream(vrs, vl + 4096u * (e >> 2) + 256u * (e & 3) + 128u * h);
+}
+
+// One fp8 tile whose K codes have landed in the wave's LDS slot ks_lds (as compute_tile).
 template <int NT>
-__device__ __forceinline__ void wait_and_compute8(const VTile8& b, const u32x4_t* ks_lds, int p0,
-                                                  int Lmin, const int (&Lcol)[NT],
-                                                  const bf16x8_t (&qb)[NT][8], float scale_log2,
-                                                  int c, int g4, float (&m)[NT], float (&l)[NT],
-                                                  f32x4_t (&acc)[NT][16]) {
-  vmcnt_wait<16>();  // the 8 K loads were issued before the 16 V loads
+__device__ __forceinline__ void compute_tile8(const VTile8& b, const u32x4_t* ks_lds, int p0,
+                                              int Lmin, const int (&Lcol)[NT],
+                                              const bf16x8_t (&qb)[NT][8], float scale_log2,
+                                              int c, int g4, float (&m)[NT], float (&l)[NT],
+                                              f32x4_t (&acc)[NT][16]) {
   wave_lds_fence();
   f32x4_t sacc[NT][2];
   qk_tile8<NT>(ks_lds, qb, c, g4, sacc);
@@ -307,7 +350,12 @@ __device__ __forceinline__ void wait_and_compute8(const VTile8& b, const u32x4_t
   }
 }
 
-// LDS: per-wave K tiles during the loop; reused for the cross-wave merge afterwards.
+// LDS: per-wave K tiles during the loop; reused for the cross-wave merge afterwards. The tile
+// loop keeps the next tile's K in flight in a second slot (two 16 KB bf16 slots, or two 8 KB fp8
+// slots, per wave); the fused prep + decode keeps one bf16 slot (its prep needs the rest).
+constexpr int lds_wave_bytes(bool fused, bool kv8) {
+  return kv8 ? 2 * TILE * HD : (fused ? 1 : 2) * TILE * HD * 2;
+}
 template <int WAVES>
 constexpr int lds_k_bytes() { return WAVES * TILE * HD * 2; }  // 16 KB per wave
 
@@ -526,7 +574,7 @@ __device__ __forceinline__ void fused_prep_compute(const PrepIn& pin, int s, int
 // write one row, they write the same bits). kc/vc are written here, so they are not __restrict__.
 template <int NT, bool FUSED = false, bool MULTI = true, bool KV8 = false,
           int WAVES = waves_for<NT>()>
-__global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_eu(NT == 1 && !FUSED ? 2 : 1, 2)))
+__global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_eu(NT == 1 && KV8 ? 2 : 1, 2)))
 attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf16* vc,
                      const int* __restrict__ pos_ptr, float* __restrict__ part_o,
                      float* __restrict__ part_ml, int n, int Hq, int Hkv, int max_len, int NS,
@@ -572,11 +620,13 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
   const bool attend = attendA || attendB;  // uniform per workgroup
   if (!attend && !(FUSED && s == 0)) return;  // (slice 0 of the fused kernel still writes q_out)
 
-  __shared__ __attribute__((aligned(256))) char lds[lds_k_bytes<WAVES>()];  // 16 KB per wave
+  constexpr int WAREA = lds_wave_bytes(FUSED, KV8);  // this wave's K slots
+  static_assert(WAREA >= lds_k_bytes<1>(), "each wave's area holds its merge buffer (16 KB)");
+  __shared__ __attribute__((aligned(256))) char lds[WAVES * WAREA];
   __shared__ float s_m[WAVES][16 * NT], s_l[WAVES][16 * NT];
   static_assert(!(FUSED && KV8), "the fused prep writes a bf16 cache");
   static_assert(!FUSED || NT == 1, "the fused prep runs at one column tile");
-  u32x4_t* ks_lds = reinterpret_cast<u32x4_t*>(lds) + w * TILE * ROW_CHUNKS;
+  u32x4_t* ks_lds = reinterpret_cast<u32x4_t*>(lds + w * WAREA);
   constexpr int ELEM = KV8 ? 1 : 2;  // bytes per cache value
   const size_t head_off = (size_t)g * max_len * HD * ELEM;  // bytes
   const char* kbase = reinterpret_cast<const char*>(kc) + head_off;  // this KV head's K rows
@@ -643,28 +693,83 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
       for (int a = 0; a < 16; ++a) acc[ct][a] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
 
+    // Look-ahead tile loop (every partials kernel but the fused one). A wave's tiles are p0,
+    // p0 + STEP, ...; K runs one tile ahead in the second of the wave's two LDS slots: as soon as
+    // tile k's K has landed, tile k+1's K is issued, and tile k+1's V right after tile k's
+    // O^T += V^T P^T has consumed the V registers. Issue order K0, V0 | K1 | V1 | K2 | ...: at the
+    // top of each tile only that tile's V (16 loads) can have been issued after its K. Tile
+    // k+1's K lands during tile k's arithmetic, and the last data a wave waits for is a V tile,
+    // whose flight S^T and the softmax of its tile overlap. The last tile is peeled, so no load
+    // is issued past the pass (a load with an empty resource still costs issue and return
+    // slots: always issuing the next K cost 0.3-0.5 us per call). Same arithmetic as the
+    // single-slot loop, bit for bit.
+    constexpr int STEP = WAVES * TILE;
+    auto lds_tile = [&](uint32_t b) __attribute__((always_inline)) {
+      return (const u32x4_t*)((__attribute__((address_space(3))) const u32x4_t*)(uintptr_t)b);
+    };
     if constexpr (KV8) {
       VTile8 buf;
       const TileLanes8 tl(lane);
-      for (int p0 = P.beg + w * TILE; p0 < P.end; p0 += WAVES * TILE) {
-        load_tile8(buf, ks_s, tile_rsrc(kbase, p0, P.end, HD), tile_rsrc(vbase, p0, P.end, HD), tl);
-        wait_and_compute8<NT>(buf, ks_lds, p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
-      }
-    } else {
       int p0 = P.beg + w * TILE;
-      if constexpr (FUSED) {
-        if (first && pf) {  // the tile loaded before the prep
-          fused_place_tile(kpf, buf, ks_lds, fused_lds<NT>().knew, fused_lds<NT>().vnew, p0,
-                           P.end, pos0, t_lo, t_hi, lane, c, g4);
-          wait_and_compute<NT>(buf, ks_lds, p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
-          p0 += WAVES * TILE;
+      if (p0 < P.end) {
+        uint32_t cur = ks_s, nxt = ks_s + TILE * HD;  // two 8 KB slots
+        issue_k8(cur, tile_rsrc(kbase, p0, P.end, HD), tl);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_v8(buf, tile_rsrc(vbase, p0, P.end, HD), tl);
+        for (; p0 + STEP < P.end; p0 += STEP) {
+          vmcnt_wait<16>();  // this tile's K: its V (16 loads) may remain
+          __builtin_amdgcn_sched_barrier(0);
+          issue_k8(nxt, tile_rsrc(kbase, p0 + STEP, P.end, HD), tl);
+          __builtin_amdgcn_sched_barrier(0);
+          compute_tile8<NT>(buf, lds_tile(cur), p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l,
+                            acc);
+          __builtin_amdgcn_sched_barrier(0);
+          issue_v8(buf, tile_rsrc(vbase, p0 + STEP, P.end, HD), tl);
+          const uint32_t t = cur;
+          cur = nxt;
+          nxt = t;
         }
+        vmcnt_wait<16>();
+        compute_tile8<NT>(buf, lds_tile(cur), p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
+      }
+    } else if constexpr (FUSED) {
+      // single slot: the fused prep's LDS leaves room for one K tile per wave
+      int p0 = P.beg + w * TILE;
+      if (first && pf) {  // the tile loaded before the prep
+        fused_place_tile(kpf, buf, ks_lds, fused_lds<NT>().knew, fused_lds<NT>().vnew, p0, P.end,
+                         pos0, t_lo, t_hi, lane, c, g4);
+        wait_and_compute<NT>(buf, ks_lds, p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
+        p0 += STEP;
       }
       const TileLanes tl(lane);
-      for (; p0 < P.end; p0 += WAVES * TILE) {
+      for (; p0 < P.end; p0 += STEP) {
         load_tile(buf, ks_s, tile_rsrc(kbase, p0, P.end, HD * 2),
                   tile_rsrc(vbase, p0, P.end, HD * 2), tl);
         wait_and_compute<NT>(buf, ks_lds, p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
+      }
+    } else {
+      const TileLanes tl(lane);
+      int p0 = P.beg + w * TILE;
+      if (p0 < P.end) {
+        uint32_t cur = ks_s, nxt = ks_s + TILE * HD * 2;  // two 16 KB slots
+        issue_k(cur, tile_rsrc(kbase, p0, P.end, HD * 2), tl);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_v(buf, tile_rsrc(vbase, p0, P.end, HD * 2), tl);
+        for (; p0 + STEP < P.end; p0 += STEP) {
+          vmcnt_wait<16>();  // this tile's K: its V (16 loads) may remain
+          __builtin_amdgcn_sched_barrier(0);
+          issue_k(nxt, tile_rsrc(kbase, p0 + STEP, P.end, HD * 2), tl);
+          __builtin_amdgcn_sched_barrier(0);
+          compute_tile<NT>(buf, lds_tile(cur), p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l,
+                           acc);
+          __builtin_amdgcn_sched_barrier(0);
+          issue_v(buf, tile_rsrc(vbase, p0 + STEP, P.end, HD * 2), tl);
+          const uint32_t t = cur;
+          cur = nxt;
+          nxt = t;
+        }
+        vmcnt_wait<16>();
+        compute_tile<NT>(buf, lds_tile(cur), p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
       }
     }
 
@@ -673,10 +778,13 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
     for (int ct = 0; ct < NT; ++ct) l[ct] = group4_sum(l[ct]);
 
     static_assert(WAVES == 4, "merge layout assumes 4 waves");
-    f32x4_t (*s_acc)[16][WAVE] = reinterpret_cast<f32x4_t (*)[16][WAVE]>(lds);
     if constexpr (NT == 1) {
+      // s_acc[v]: the first 16 KB of wave v's K slots
+      auto s_acc = [&](int v, int a) __attribute__((always_inline)) -> f32x4_t& {
+        return reinterpret_cast<f32x4_t*>(lds + v * WAREA)[a * WAVE + lane];
+      };
       // One barrier: each wave parks (m, l) and the accumulators of the pass's columns in its own
-      // K tile's LDS (s_acc[w] is exactly that region, which no other wave touches), then thread
+      // K slots' LDS (s_acc(w, .) lies there, which no other wave touches), then thread
       // (w, lane) merges h = w/2, i in [4(w&1), +4) over waves 0..3 in that order and writes
       // 4 x 16 bytes: dims 128h + 32g4 + 8ii + 4(w&1) + [0, 4) for ii = 0..3. Same arithmetic
       // and order as the NT >= 2 merge below, so the bits do not depend on NT.
@@ -688,7 +796,7 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
       }
       if (mine) {
 #pragma unroll
-        for (int a = 0; a < 16; ++a) s_acc[w][a][lane] = acc[0][a];
+        for (int a = 0; a < 16; ++a) s_acc(w, a) = acc[0][a];
       }
       __syncthreads();
       if (!mine) return;
@@ -714,7 +822,7 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
       for (int k = 0; k < 4; ++k) {
         f32x4_t sum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int v = 0; v < WAVES; ++v) sum += s_acc[v][8 * h + i0 + k][lane] * wsc[v];
+        for (int v = 0; v < WAVES; ++v) sum += s_acc(v, 8 * h + i0 + k) * wsc[v];
         mo[k] = sum;
       }
       float* dst = part_o + (((size_t)t * Hq + head) * NS + s) * HD + 128 * h + 32 * g4 + i0;
@@ -760,7 +868,8 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
     // other columns stay idle, which keeps the LDS traffic to what the merge needs), one barrier,
     // then thread (w, lane) merges h = w/2, i in [4(w&1), +4) over waves 0..3 in that order and
     // writes 4 x 16 bytes: dims 128h + 32g4 + 8ii + 4(w&1) + [0, 4) for ii = 0..3.
-    static_assert(WAVES * 16 * WAVE * 16 <= lds_k_bytes<WAVES>(), "merge buffer aliases the K tiles");
+    f32x4_t (*s_acc)[16][WAVE] = reinterpret_cast<f32x4_t (*)[16][WAVE]>(lds);
+    static_assert(WAVES * 16 * WAVE * 16 <= WAVES * WAREA, "merge buffer aliases the K tiles");
 #pragma unroll
     for (int ct = 0; ct < NT; ++ct) {
       const int col = ct * 16 + c;

@@ -528,13 +528,13 @@ def test_gdn_contract(native):
 
 
 def test_default_splits_policy():
-    """Split count: 3/4 of the CUs per KV head for a bf16 cache, one workgroup per CU for fp8,
+    """Split count: 13/16 of the CUs in workgroups for a bf16 cache, one workgroup per CU for fp8,
     never a slice shorter than 32 positions."""
     import qengine_amd as qa
-    assert qa.default_splits(16384, 4, cus=256) == 48
-    assert qa.default_splits(131072, 4, cus=256) == 48
+    assert qa.default_splits(16384, 4, cus=256) == 52
+    assert qa.default_splits(131072, 4, cus=256) == 52
     assert qa.default_splits(16384, 4, cus=256, kv8=True) == 64
-    assert qa.default_splits(16384, 8, cus=256) == 24
+    assert qa.default_splits(16384, 8, cus=256) == 26
     assert qa.default_splits(1000, 4, cus=256) == 32  # ceil(1000 / 32)
     assert qa.default_splits(64, 4, cus=256, kv8=True) == 2
     assert qa.default_splits(1, 64, cus=4) == 1
