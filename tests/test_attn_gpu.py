@@ -133,35 +133,69 @@ def test_config1_prep_and_decode(native):
     assert ok, (mx, mean)
 
 
+def _ns(ns, max_len, kv8=False):
+    """A split count, or "default": the count the engine and the bench use (default_splits)."""
+    import qengine_amd as qa
+    return qa.default_splits(max_len, 4, kv8=kv8) if ns == "default" else ns
+
+
+_ORACLE = {}
+
+
+def cached_oracle(key, case):
+    """The oracle's output for a case built from a seed (several split counts share it)."""
+    if key not in _ORACLE:
+        _ORACLE[key] = oracle_decode(case)
+    return _ORACLE[key]
+
+
 @pytest.mark.parametrize("L", [1024, 4096, 16384, 32768])
-@pytest.mark.parametrize("ns", [16, 64])
+@pytest.mark.parametrize("ns", [16, 64, "default"])
 def test_config2_split_sweep(native, L, ns):
-    """cfg 2: split-KV decode at KV 4k/16k/32k (and cfg 1's 1k), N(0,1) cache, seeded."""
+    """cfg 2: split-KV decode at KV 4k/16k/32k (and cfg 1's 1k), N(0,1) cache, seeded, at the
+    split count the bench times (default_splits: 52 on MI355X) and at 16 and 64."""
     case = decode_case(seed=L, hq=24, hkv=4, pos=L - 1, n=1)
-    out = gpu_decode(native, case, ns)
-    ok, mx, mean = attn_close(out, oracle_decode(case))
+    out = gpu_decode(native, case, _ns(ns, L))
+    ok, mx, mean = attn_close(out, cached_oracle(("cfg2", L), case))
     assert ok, (L, ns, mx, mean)
 
 
+@pytest.mark.parametrize("L,n", [(4096, 2), (16384, 2), (16384, 5), (32768, 3)])
+def test_default_split_rows_bit_exact(native, L, n):
+    """At the default split count, row t of an n-row call (one and two MFMA column tiles) equals
+    a 1-row call at position pos+t bit for bit, and the call matches the oracle."""
+    ns = _ns("default", L)
+    case = decode_case(seed=L + n, hq=24, hkv=4, pos=L - n, n=n, max_len=L)
+    out = gpu_decode(native, case, ns)
+    ok, mx, mean = attn_close(out, oracle_decode(case))
+    assert ok, (mx, mean)
+    for t in range(n):
+        o1 = gpu_decode(native, case, ns, pos=case.pos + t, rows=slice(t, t + 1))
+        assert torch.equal(o1[0], out[t]), t
+
+
+@pytest.mark.parametrize("ns", [512, "default"])
 @pytest.mark.parametrize("adversarial", [False, True])
-def test_config4_long_context(native, adversarial):
-    """cfg 4: KV 131072 (537 MB of K+V); the adversarial variant scales 1% of key rows by 8."""
+def test_config4_long_context(native, adversarial, ns):
+    """cfg 4: KV 131072 (537 MB of K+V); the adversarial variant scales 1% of key rows by 8; at
+    512 splits and at the default count (the bench's)."""
     L = 131072
     case = decode_case(seed=4, hq=24, hkv=4, pos=L - 1, n=1,
                        key_scale_frac=0.01 if adversarial else 0.0)
-    out = gpu_decode(native, case, 512)
-    ok, mx, mean = attn_close(out, oracle_decode(case))
-    assert ok, (adversarial, mx, mean)
+    out = gpu_decode(native, case, _ns(ns, L))
+    ok, mx, mean = attn_close(out, cached_oracle(("cfg4", adversarial), case))
+    assert ok, (adversarial, ns, mx, mean)
 
 
-def test_config3_mtp_verify(native):
+@pytest.mark.parametrize("ns", [16, "default"])
+def test_config3_mtp_verify(native, ns):
     """cfg 3: 5 rows (1 accepted + 4 drafts) at pos 4096, causal among themselves, over 4096
     cached + 5 new rows. Rows must be bit-identical to 5 sequential 1-row decodes, so argmax over a
     seeded bf16 projection [151936 x 5120] . [5120 x 6144] of the outputs is identical; both
-    also stay within tolerance of the oracle."""
+    also stay within tolerance of the oracle. At 16 splits and at the bench's default count."""
     C = native
     case = decode_case(seed=3, hq=24, hkv=4, pos=4096, n=5, max_len=4096 + 64)
-    ns = 16
+    ns = _ns(ns, case.kc.shape[1])
     verify = gpu_decode(C, case, ns)
     seq = torch.cat([gpu_decode(C, case, ns, pos=case.pos + t, rows=slice(t, t + 1))
                      for t in range(5)])

@@ -28,12 +28,12 @@ def plain(engine):
     return toks
 
 
-def _drafter(plain, kind):
+def _drafter(plain, kind, k=3):
     P = len(PROMPT)
 
     def d(pos, last):
         out = []
-        for j in range(3):
+        for j in range(k):
             idx = pos + 1 + j - P  # index into the generated tokens of position pos + 1 + j
             right = plain[idx] if 0 <= idx < len(plain) else 0
             if kind == "right" or (kind == "mixed" and (pos + j) % 3 != 0):
@@ -114,3 +114,44 @@ def test_hybrid_state_after_spec_equals_plain(hybrid, hybrid_plain):
         if mode == "spec":
             hybrid.reset()
     assert all(torch.equal(a, b) for a, b in zip(*states))
+
+
+# ---------------------------------------------------------------- the reference's length
+# tests/test_spec.py:57-67 of the reference checks spec == plain over 1,024 generated tokens for
+# k = 1..4 drafts. Here 1,800 tokens on a 2,048-position cache at the default split count (52 on
+# MI355X): a row attending L positions uses slices of split_size(L, 52), 32 positions up to
+# L = 1,664 and 64 after, so the run crosses a change of slice size, where verify passes hold
+# rows on both sides of it (one pass per size inside the kernel).
+N_LONG = 1800
+
+
+@pytest.fixture(scope="module")
+def long_engine(native):
+    return MiniEngine(layers=2, hidden=1024, inter=2048, vocab=4096, max_len=2048, seed=7)
+
+
+@pytest.fixture(scope="module")
+def long_plain(long_engine):
+    toks = long_engine.generate_plain(PROMPT, N_LONG)
+    assert len(set(toks)) > 3, toks
+    return toks
+
+
+def test_long_run_crosses_a_slice_size_change(long_engine):
+    import qengine_amd as qa
+    ns = long_engine.part_o.shape[2]
+    assert ns == qa.default_splits(2048, 4)
+    first, last = len(PROMPT) + 1, len(PROMPT) + N_LONG
+    assert qa.split_size(first, ns) < qa.split_size(last, ns)
+
+
+@pytest.mark.parametrize("k", [1, 2, 3, 4])
+@pytest.mark.parametrize("kind", ["mixed", "right"])
+def test_spec_equals_plain_long(long_engine, long_plain, k, kind):
+    toks, passes, ctl = long_engine.generate_spec(PROMPT, N_LONG,
+                                                  _drafter(long_plain, kind, k), k=k)
+    assert toks == long_plain
+    if kind == "mixed":
+        assert 0 < ctl[5] < k * passes
+    else:
+        assert passes <= (N_LONG + k - 1) // (k + 1) + 2

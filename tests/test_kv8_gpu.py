@@ -222,3 +222,53 @@ def test_prep_fp8_chunk_equals_eight_row_preps(native):
     assert torch.equal(q_a.view(torch.int16), q_b.view(torch.int16))
     assert torch.equal(kc_a.view(torch.uint8), kc_b.view(torch.uint8))
     assert torch.equal(vc_a.view(torch.uint8), vc_b.view(torch.uint8))
+
+
+@pytest.mark.parametrize("L", [16384, 32768])
+def test_fp8_decode_default_splits(native, L):
+    """The fp8 decode at the split count the bench times on an fp8 cache (default_splits with
+    kv8: 64 on MI355X), one row at KV 16k / 32k: with scales of 1 bit-identical to the bf16 decode
+    on the dequantized cache, and with scales of 1/8 within tolerance of the oracle."""
+    import qengine_amd as qa
+    ns = qa.default_splits(L, 4, kv8=True)
+    case = decode_case(seed=L + 8, hq=24, hkv=4, pos=L - 1, n=1, max_len=L)
+    kc8, vc8 = quantize_cache(case.kc, 1.0), quantize_cache(case.vc, 1.0)
+    kd = K8.dequantize(kc8.view(torch.uint8), 1.0).to(BF)
+    vd = K8.dequantize(vc8.view(torch.uint8), 1.0).to(BF)
+    a = run_fp8(native, case.q, case.qg, kc8, vc8, case.pos, ns, 1.0, 1.0)
+    b = run_bf16(native, case.q, case.qg, kd, vd, case.pos, ns)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    ks = vs = 0.125
+    kc8, vc8 = quantize_cache(case.kc, ks), quantize_cache(case.vc, vs)
+    out = run_fp8(native, case.q, case.qg, kc8, vc8, case.pos, ns, ks, vs)
+    ref = O.attn_decode(case.q, K8.dequantize(kc8.view(torch.uint8), ks),
+                        K8.dequantize(vc8.view(torch.uint8), vs), case.pos, case.qg, case.hq)
+    ok, mx, mean = attn_close(out, ref)
+    assert ok, (mx, mean)
+
+
+def _all_code_cache(hkv, max_len, shift):
+    """fp8 cache whose values cycle through all 254 non-NaN E4M3FN codes (0x00-0x7e, 0x80-0xfe:
+    zeros, subnormals, normals up to +-448), in a different order per element offset."""
+    codes = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], dtype=np.uint8)
+    assert codes.size == 254
+    idx = (np.arange(hkv * max_len * D, dtype=np.int64) * 97 + shift) % codes.size
+    return torch.from_numpy(codes[idx].reshape(hkv, max_len, D)).view(F8)
+
+
+@pytest.mark.parametrize("n,pos,max_len,ns", [(1, 1200, 1201, 16), (2, 3000, 3002, 64),
+                                              (5, 700, 705, 8), (7, 2000, 2007, 16)])
+def test_fp8_every_code_equals_bf16(native, n, pos, max_len, ns):
+    """K and V caches holding every finite E4M3FN code (the kernels' conversion runs on all of
+    them: zeros, subnormals, the largest magnitudes), scales of 1: the fp8 decode (one-tile,
+    two-tile and multi-column kernels) is bit-identical to the bf16 decode on the dequantized
+    cache. q is scaled down so that scores against keys up to 448 stay moderate."""
+    case = decode_case(seed=pos + n, hq=24, hkv=4, pos=pos, n=n, max_len=max_len)
+    kc8, vc8 = _all_code_cache(4, max_len, 5), _all_code_cache(4, max_len, 71)
+    kd = K8.dequantize(kc8.view(torch.uint8), 1.0).to(BF)
+    vd = K8.dequantize(vc8.view(torch.uint8), 1.0).to(BF)
+    q = (case.q.float() * 0.01).to(BF)
+    a = run_fp8(native, q, case.qg, kc8, vc8, case.pos, ns, 1.0, 1.0)
+    b = run_bf16(native, q, case.qg, kd, vd, case.pos, ns)
+    assert torch.isfinite(b.float()).all()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
