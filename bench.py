@@ -141,6 +141,7 @@ def bench_length_fp8(torch, C, qa, L: int, steps: int, warmup: int) -> dict:
     del sets, full, part
     torch.cuda.empty_cache()
     return {"us_per_layer": round(us_layer, 3), "GBps": round(b_layer / (us_layer * 1e3), 1),
+            "kv_rotation_MB": round(nsets * LAYERS * L * 2048 / 2 ** 20, 1),
             "partials_us": round(us_part, 3),
             "partials_GBps": round(b_part / (us_part * 1e3), 1),
             "partials_frac": round(b_part / (us_part * 1e3) / HBM_PEAK_GBS, 4)}
@@ -159,6 +160,9 @@ def capture(torch, fn):
     return g
 
 
+# (workgroups per KV head, 16-byte loads in flight per thread and tensor) of the floor sweep;
+# on MI355X the fastest 67-134 MB reads used >= 512 workgroups and 4-8 loads
+STREAM_SWEEP = ((52, 16), (64, 16), (128, 4), (128, 8), (256, 4), (256, 8), (512, 4), (512, 8))
 MIN_WARMUP_REPLAYS = 30  # the reference's time_graph warms each graph up 30 times
 MIN_WARMUP_SECONDS = 0.1  # and at least this long per graph: clocks ramp over tens of ms
 # MFMA-bound graphs (the prefill legs) take longer to reach steady clocks: after 0.1 s of replays
@@ -232,6 +236,10 @@ def bench_length(torch, C, qa, L: int, steps: int, warmup: int, ns: int | None):
     def probe_all(s):
         for k, v in zip(s.kc, s.vc):
             capi.kv_stream_probe(k, v, s.pos, HKV, L, ns, sink)
+
+    def sweep_all(s, gph, depth):
+        for k, v in zip(s.kc, s.vc):
+            capi.kv_stream_sweep(k, v, s.pos, HKV, L, gph, depth, sink)
     full = [capture(torch, s.decode_all) for s in sets]
     part = [capture(torch, s.partials_all) for s in sets]
     probe = [capture(torch, lambda s=s: probe_all(s)) for s in sets]
@@ -243,6 +251,15 @@ def bench_length(torch, C, qa, L: int, steps: int, warmup: int, ns: int | None):
     us_layer = t_full.median * 1e3 / LAYERS
     us_part = t_part.median * 1e3 / LAYERS
     us_probe = t_probe.median * 1e3 / LAYERS
+    # the one-launch floor whatever the grid: the same bytes swept over grid size (workgroups per
+    # KV head) and loads in flight per thread; the fastest configuration is the floor
+    stream = {}
+    for gph, depth in STREAM_SWEEP:
+        gs = [capture(torch, lambda s=s: sweep_all(s, gph, depth)) for s in sets]
+        stream[f"{gph}x{depth}"] = round(
+            time_graphs(torch, gs, steps, warmup).median * 1e3 / LAYERS, 3)
+        del gs
+    best = min(stream, key=stream.get)
     res = {
         "L": L, "NS": ns, "split_size": qa.split_size(L, ns), "kv_rotation_MB":
             round(nsets * LAYERS * L * 4096 / 2 ** 20, 1),
@@ -253,6 +270,8 @@ def bench_length(torch, C, qa, L: int, steps: int, warmup: int, ns: int | None):
         "partials_GBps": alg_bytes_partials(L) / (us_part * 1e3),
         "partials_us_mean": t_part.mean * 1e3 / LAYERS,
         "kv_stream_probe_us": us_probe,
+        "stream_sweep_us": stream,
+        "best_stream_us": stream[best], "best_stream_cfg": best,
         "combine_us": t_comb.median * 1e3 / LAYERS,
     }
     res["frac"] = res["GBps"] / HBM_PEAK_GBS
@@ -263,19 +282,25 @@ def bench_length(torch, C, qa, L: int, steps: int, warmup: int, ns: int | None):
 
 
 def ceiling(sweep, node_us: float) -> dict:
-    """What any design can reach on this box, per KV length, in µs per layer-call: the streaming
-    probe on the partials grid is the floor of one launch that reads the K/V bytes; adding one
-    empty graph node gives the floor of a two-launch layer-call (partials + combine), and the
-    combine alone is what this build's second node costs; the BASELINE target is 75% of 8 TB/s
-    on the algorithmic bytes."""
+    """What any design can reach on this box, per KV length, in µs per graph node: the fastest
+    streaming read of the K/V bytes over a sweep of grids and load depths is the floor of one
+    launch that reads them (best_stream_us); the same read on the partials kernel's own grid is
+    kv_stream_probe_us; adding one empty graph node gives the floor of a two-launch layer-call
+    (partials + combine); the combine alone is what this build's second node costs; the BASELINE
+    target is 75% of 8 TB/s on the algorithmic bytes."""
     out = {"graph_node_us": round(node_us, 3), "per_L": {}}
     for r in sweep:
         L = r["L"]
         out["per_L"][str(L)] = {
+            "best_stream_us": r["best_stream_us"], "best_stream_cfg": r["best_stream_cfg"],
             "kv_stream_probe_us": round(r["kv_stream_probe_us"], 3),
-            "one_launch_floor_us": round(r["kv_stream_probe_us"], 3),
-            "two_launch_floor_us": round(r["kv_stream_probe_us"] + node_us, 3),
+            "one_launch_floor_us": r["best_stream_us"],
+            "two_launch_floor_us": round(r["best_stream_us"] + node_us, 3),
+            "partials_us": round(r["partials_us"], 3),
+            "partials_minus_best_stream_us": round(r["partials_us"] - r["best_stream_us"], 3),
             "measured_us": round(r["us_per_layer"], 3),
+            "measured_minus_two_launch_floor_us": round(
+                r["us_per_layer"] - r["best_stream_us"] - node_us, 3),
             "combine_alone_us": round(r["combine_us"], 3),
             "target_75pct_us": round(alg_bytes_layer(L) / (0.75 * HBM_PEAK_GBS * 1e3), 3)}
     return out
@@ -297,8 +322,20 @@ def time_fn_graph(torch, fn, steps: int, warmup: int,
     return time_graphs(torch, [capture(torch, fn)], steps, warmup, min_seconds).median
 
 
+def rotated(bytes_per_set: int) -> int:
+    """Sets of LAYERS caches (one graph each, replayed round-robin) so that >= 512 MB of distinct
+    KV bytes rotate: the 256 MB Infinity Cache cannot serve a repeated read."""
+    return max(1, math.ceil(ROTATE_BYTES / bytes_per_set))
+
+
+def time_sets(torch, fns, steps: int, warmup: int) -> float:
+    """ms per replay (median) over one graph per set, replayed round-robin."""
+    return time_graphs(torch, [capture(torch, f) for f in fns], steps, warmup).median
+
+
 def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
-    """The other BASELINE configs, each timed as graph replays on the GPU (values per call)."""
+    """The other BASELINE configs, each timed as graph replays on the GPU (values per call). Every
+    HBM-bound leg rotates >= 512 MB of distinct KV (kv_rotation_MB)."""
     dev, BF = "cuda", torch.bfloat16
     gen = torch.Generator(device=dev).manual_seed(1)
     res = {}
@@ -311,8 +348,10 @@ def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
 
     # cfg 1: prep + decode, one row at KV 1024, 16 layers per step
     L, nl = 1024, 16
-    kcs = [rnd(HKV, L, D) for _ in range(nl)]
-    vcs = [rnd(HKV, L, D) for _ in range(nl)]
+    nsets = rotated(nl * L * 4096)
+    sets = [([rnd(HKV, L, D) for _ in range(nl)], [rnd(HKV, L, D) for _ in range(nl)])
+            for _ in range(nsets)]
+    rot_mb = round(nsets * nl * L * 4096 / 2 ** 20, 1)
     proj = rnd(1, HQ * 2 * D + 2 * HKV * D + 8, scale=3.0)
     qg, k, v = proj[:, :HQ * 2 * D], proj[:, HQ * 2 * D:HQ * 2 * D + HKV * D], proj[:, HQ * 2 * D + HKV * D:HQ * 2 * D + 2 * HKV * D]
     q = torch.empty(1, HQ * D, dtype=BF, device=dev)
@@ -321,21 +360,23 @@ def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
     po, pml = qa.alloc_partials(1, HQ, ns, dev)
     pos = torch.tensor([L - 1], dtype=torch.int32, device=dev)
 
-    def cfg1():
+    def cfg1(kcs, vcs):
         for kk, vv in zip(kcs, vcs):
             C.attn_prep(qg, k, v, qnw, knw, inv, pos, q, kk, vv, 1e-6)
             C.attn_decode(q, kk, vv, pos, qg, po, pml, out)
-    us = time_fn_graph(torch, cfg1, steps, warmup) * 1e3 / nl
+    us = time_sets(torch, [lambda s=s: cfg1(*s) for s in sets], steps, warmup) * 1e3 / nl
     res["cfg1_prep_decode_1k"] = {"us_per_layer": round(us, 3),
-                                  "GBps": round((alg_bytes_layer(L) + 45056) / (us * 1e3), 1)}
+                                  "GBps": round((alg_bytes_layer(L) + 45056) / (us * 1e3), 1),
+                                  "kv_rotation_MB": rot_mb}
 
-    def cfg1_fused():
+    def cfg1_fused(kcs, vcs):
         for kk, vv in zip(kcs, vcs):
             C.attn_prep_decode(qg, k, v, qnw, knw, inv, pos, q, kk, vv, 1e-6, po, pml, out)
-    us = time_fn_graph(torch, cfg1_fused, steps, warmup) * 1e3 / nl
+    us = time_sets(torch, [lambda s=s: cfg1_fused(*s) for s in sets], steps, warmup) * 1e3 / nl
     res["cfg1_prep_decode_1k_fused"] = {"us_per_layer": round(us, 3),
-                                        "GBps": round((alg_bytes_layer(L) + 45056) / (us * 1e3), 1)}
-    del kcs, vcs
+                                        "GBps": round((alg_bytes_layer(L) + 45056) / (us * 1e3), 1),
+                                        "kv_rotation_MB": rot_mb}
+    del sets
 
     # prep + decode per layer at KV 16384 (16 layers on distinct caches), separate and fused ops
     L, nl = 16384, 16
@@ -356,26 +397,29 @@ def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
     for name, fn in (("prep_decode_16k", sep16), ("prep_decode_16k_fused", fused16)):
         us = time_fn_graph(torch, fn, steps, warmup) * 1e3 / nl
         res[name] = {"us_per_layer": round(us, 3),
-                     "GBps": round((alg_bytes_layer(L) + 45056) / (us * 1e3), 1)}
+                     "GBps": round((alg_bytes_layer(L) + 45056) / (us * 1e3), 1),
+                     "kv_rotation_MB": round(nl * L * 4096 / 2 ** 20, 1)}
     del kcs, vcs
 
     # cfg 3: MTP verify, 5 rows at pos 4096 over 4096 cached + 5 new positions
     L, n, nl = 4096 + 5, 5, 16
-    kcs = [rnd(HKV, L, D) for _ in range(nl)]
-    vcs = [rnd(HKV, L, D) for _ in range(nl)]
+    nsets = rotated(nl * L * 4096)
+    sets = [([rnd(HKV, L, D) for _ in range(nl)], [rnd(HKV, L, D) for _ in range(nl)])
+            for _ in range(nsets)]
     q5, qg5 = rnd(n, HQ * D), rnd(n, HQ * 2 * D)
     out5 = torch.empty(n, HQ * D, dtype=BF, device=dev)
     ns = qa.default_splits(L, HKV)
     po5, pml5 = qa.alloc_partials(n, HQ, ns, dev)
     pos5 = torch.tensor([4096], dtype=torch.int32, device=dev)
 
-    def cfg3():
+    def cfg3(kcs, vcs):
         for kk, vv in zip(kcs, vcs):
             C.attn_decode(q5, kk, vv, pos5, qg5, po5, pml5, out5)
-    us = time_fn_graph(torch, cfg3, steps, warmup) * 1e3 / nl
+    us = time_sets(torch, [lambda s=s: cfg3(*s) for s in sets], steps, warmup) * 1e3 / nl
     res["cfg3_mtp_verify_5rows_4k"] = {"us_per_layer": round(us, 3),
-                                       "GBps": round(alg_bytes_layer(L, n) / (us * 1e3), 1)}
-    del kcs, vcs
+                                       "GBps": round(alg_bytes_layer(L, n) / (us * 1e3), 1),
+                                       "kv_rotation_MB": round(nsets * nl * L * 4096 / 2 ** 20, 1)}
+    del sets
 
     # MTP verify at 8 rows (7 drafts) at pos 4096 and 16384, on bf16 and on fp8 caches: 48 columns
     # at GQA 6, the multi-column kernel (its fp8 mode for the second)
@@ -389,20 +433,24 @@ def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
         for fp8 in (False, True):
             ns = qa.default_splits(L, HKV, kv8=fp8)
             po8, pml8 = qa.alloc_partials(n, HQ, ns, dev)
-            kcs = [codes(L) if fp8 else rnd(HKV, L, D) for _ in range(nl)]
-            vcs = [codes(L) if fp8 else rnd(HKV, L, D) for _ in range(nl)]
+            per_pos = 2048 if fp8 else 4096
+            nsets = rotated(nl * L * per_pos)
+            sets = [([codes(L) if fp8 else rnd(HKV, L, D) for _ in range(nl)],
+                     [codes(L) if fp8 else rnd(HKV, L, D) for _ in range(nl)])
+                    for _ in range(nsets)]
 
-            def verify8():
+            def verify8(kcs, vcs, fp8=fp8, po8=po8, pml8=pml8):
                 for kk, vv in zip(kcs, vcs):
                     if fp8:
                         C.attn_decode_fp8(q8, kk, vv, pos8, qg8, po8, pml8, out8, 1 / 16, 1 / 16)
                     else:
                         C.attn_decode(q8, kk, vv, pos8, qg8, po8, pml8, out8)
-            us = time_fn_graph(torch, verify8, steps, warmup) * 1e3 / nl
+            us = time_sets(torch, [lambda s=s: verify8(*s) for s in sets], steps, warmup) * 1e3 / nl
             nbytes = (2048 * L + 36864 * n) if fp8 else alg_bytes_layer(L, n)
             res[f"{'fp8kv_' if fp8 else ''}verify_8rows_{P // 1024}k"] = {
-                "us_per_layer": round(us, 3), "GBps": round(nbytes / (us * 1e3), 1)}
-            del kcs, vcs
+                "us_per_layer": round(us, 3), "GBps": round(nbytes / (us * 1e3), 1),
+                "kv_rotation_MB": round(nsets * nl * L * per_pos / 2 ** 20, 1)}
+            del sets
 
     # cfg 4: KV 131072 (537 MB per layer: two layers rotate past the Infinity Cache), plus the
     # variant with 1% of key rows scaled by 8
@@ -424,29 +472,35 @@ def bench_configs(torch, C, qa, steps: int, warmup: int) -> dict:
                 C.attn_decode(q1, kk, vv, pos1, qg1, po1, pml1, out)
         us = time_fn_graph(torch, cfg4, steps, warmup) * 1e3 / nl
         res[name] = {"us_per_layer": round(us, 3), "GBps": round(alg_bytes_layer(L) / (us * 1e3), 1),
-                     "hbm_frac": round(alg_bytes_layer(L) / (us * 1e3) / HBM_PEAK_GBS, 4)}
+                     "hbm_frac": round(alg_bytes_layer(L) / (us * 1e3) / HBM_PEAK_GBS, 4),
+                     "kv_rotation_MB": round(nl * L * 4096 / 2 ** 20, 1)}
     del kcs, vcs
 
     # one row attending 4096 positions of 131072-position caches (a cache sized for long context,
     # early in a generation), 16 layers: the slices follow the attended length, so this runs like
     # the 4096-position sweep entry, not like a 131072-position cache cut into fixed slices
     Lc, La, nl = 131072, 4096, 16
-    kcs = [torch.empty(HKV, Lc, D, dtype=BF, device=dev) for _ in range(nl)]
-    vcs = [torch.empty(HKV, Lc, D, dtype=BF, device=dev) for _ in range(nl)]
-    for kk, vv in zip(kcs, vcs):
+    nsets = rotated(nl * La * 4096)  # the attended prefixes rotate
+
+    def cache_pair():
+        kk = torch.empty(HKV, Lc, D, dtype=BF, device=dev)
+        vv = torch.empty(HKV, Lc, D, dtype=BF, device=dev)
         kk[:, :La] = rnd(HKV, La, D)
         vv[:, :La] = rnd(HKV, La, D)
+        return kk, vv
+    sets = [list(zip(*[cache_pair() for _ in range(nl)])) for _ in range(nsets)]
     ns = qa.default_splits(Lc, HKV)
     poc, pmlc = qa.alloc_partials(1, HQ, ns, dev)
     posc = torch.tensor([La - 1], dtype=torch.int32, device=dev)
 
-    def short_in_long():
+    def short_in_long(kcs, vcs):
         for kk, vv in zip(kcs, vcs):
             C.attn_decode(q1, kk, vv, posc, qg1, poc, pmlc, out)
-    us = time_fn_graph(torch, short_in_long, steps, warmup) * 1e3 / nl
+    us = time_sets(torch, [lambda s=s: short_in_long(*s) for s in sets], steps, warmup) * 1e3 / nl
     res["decode_4k_in_128k_cache"] = {"us_per_layer": round(us, 3),
-                                      "GBps": round(alg_bytes_layer(La) / (us * 1e3), 1)}
-    del kcs, vcs
+                                      "GBps": round(alg_bytes_layer(La) / (us * 1e3), 1),
+                                      "kv_rotation_MB": round(nsets * nl * La * 4096 / 2 ** 20, 1)}
+    del sets
 
     for L in (4096, 16384, 32768, 131072):
         res[f"fp8kv_decode_{L // 1024}k"] = bench_length_fp8(torch, C, qa, L, steps, warmup)
@@ -835,7 +889,8 @@ def main():
         r = bench_length(torch, C, qa, L, args.steps, args.warmup, args.ns or None)
         print(f"# L={L}: {r['us_per_layer']:.2f} us/layer-call, {r['GBps']:.0f} GB/s "
               f"({100 * r['frac']:.1f}%), partials {r['partials_us']:.2f} us "
-              f"({100 * r['partials_frac']:.1f}%); stream probe {r['kv_stream_probe_us']:.2f} us",
+              f"({100 * r['partials_frac']:.1f}%); stream probe {r['kv_stream_probe_us']:.2f} us"
+              f", best stream {r['best_stream_us']:.2f} us ({r['best_stream_cfg']})",
               file=sys.stderr, flush=True)
         sweep.append(r)
     head = next(r for r in sweep if r["L"] == HEADLINE_L)

@@ -158,9 +158,20 @@ hipError_t qe_attn_decode_fp8_partials(const void* q, const void* kc8, const voi
  * heads, pos read on the device, 256 threads per workgroup, 16-byte non-temporal loads) and no
  * arithmetic: the floor of any kernel that reads those bytes with that grid. `sink` (4 bytes of
  * device memory) is written only if the folded value hits a constant.
- * Valid: max_len >= 1, Hkv >= 1, NS >= 1, max_len*512 < 2^32. */
+ * Valid: max_len >= 1, Hkv >= 1, NS >= 1, (max_len + 64)*512 < 2^32. */
 hipError_t qe_kv_stream_probe(const void* kc, const void* vc, const int* pos, int Hkv,
                               int max_len, int NS, void* sink, hipStream_t stream);
+
+/* Measurement only (no counterpart in the reference). The same K and V bytes as
+ * qe_kv_stream_probe on any grid: (grid_per_head, Hkv) workgroups of 256 threads, each streaming
+ * a 4 KB-aligned 1/grid_per_head share of its KV head's K rows and of its V rows with depth +
+ * depth sixteen-byte non-temporal loads in flight per thread, no arithmetic. Swept over the grid
+ * and depth, the fastest is the floor of any one-launch read of these bytes on the part.
+ * Valid: max_len >= 1, Hkv >= 1, 1 <= grid_per_head <= 65535, depth in {4, 8, 16},
+ * (max_len + 64)*512 < 2^32. */
+hipError_t qe_kv_stream_sweep(const void* kc, const void* vc, const int* pos, int Hkv,
+                              int max_len, int grid_per_head, int depth, void* sink,
+                              hipStream_t stream);
 
 /* Measurement only: one empty one-wave kernel. Its time per node in a hipGraph of such launches
  * is the per-launch floor every graph node pays. */

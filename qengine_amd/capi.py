@@ -32,6 +32,7 @@ SIGNATURES = {
                                  _I, _I, _I, _I, _F, _F, _P]),
     "qe_attn_split_size": (_I, [_I, _I]),
     "qe_kv_stream_probe": (_I, [_P, _P, _P, _I, _I, _I, _P, _P]),
+    "qe_kv_stream_sweep": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _P]),
     "qe_launch_probe": (_I, [_P]),
     "qe_attn_version": (ctypes.c_char_p, []),
     "qe_set_pdl_trigger": (None, [_I]),
@@ -159,6 +160,13 @@ def kv_stream_probe(kc, vc, pos, hkv, max_len, ns, sink, stream=None) -> int:
     partials kernel's grid and slicing, no arithmetic (qe_kv_stream_probe)."""
     return load().qe_kv_stream_probe(_ptr(kc), _ptr(vc), _ptr(pos), hkv, max_len, ns, _ptr(sink),
                                      _stream(stream))
+
+
+def kv_stream_sweep(kc, vc, pos, hkv, max_len, grid_per_head, depth, sink, stream=None) -> int:
+    """Measurement only: the same K/V bytes on a (grid_per_head, hkv) grid with depth + depth
+    loads in flight per thread (qe_kv_stream_sweep)."""
+    return load().qe_kv_stream_sweep(_ptr(kc), _ptr(vc), _ptr(pos), hkv, max_len, grid_per_head,
+                                     depth, _ptr(sink), _stream(stream))
 
 
 def launch_probe(stream=None) -> int:

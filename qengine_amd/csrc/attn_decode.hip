@@ -1604,8 +1604,11 @@ kv_stream_probe_kernel(const __bf16* __restrict__ kc, const __bf16* __restrict__
   const __amdgpu_buffer_rsrc_t kr = make_rsrc_uniform(kc + head, bytes);
   const __amdgpu_buffer_rsrc_t vr = make_rsrc_uniform(vc + head, bytes);
   uint32_t acc = 0;
-  for (uint32_t off = (uint32_t)beg * (HD * 2) + threadIdx.x * 16; off < bytes;
-       off += 256 * 16 * 8) {
+  // rounds of 32 KB per array from the slice start: the round count bounds the loop (an offset
+  // stepped past 2^32 would wrap)
+  const uint32_t rounds = ((uint32_t)(end - beg) * (HD * 2) + 32767u) / 32768u;
+  for (uint32_t r = 0, off = (uint32_t)beg * (HD * 2) + threadIdx.x * 16; r < rounds;
+       ++r, off += 256 * 16 * 8) {
     u32x4_t a[8], b[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -1619,17 +1622,70 @@ kv_stream_probe_kernel(const __bf16* __restrict__ kc, const __bf16* __restrict__
   if (acc == 0x9E3779B9u) sink[0] = acc;
 }
 
+// The same K and V bytes (L = min(pos+1, max_len) positions per KV head) on any grid: workgroup
+// (s, g) of (GH, Hkv) streams a 4 KB-aligned 1/GH share of KV head g's K rows and of its V rows,
+// 256 threads, DEPTH + DEPTH sixteen-byte non-temporal loads in flight per thread (one round),
+// no arithmetic. Swept over GH and DEPTH, its fastest time is the floor of reading these bytes in
+// one launch on this part, whatever the grid.
+template <int DEPTH>
+__global__ void __launch_bounds__(256)
+kv_stream_sweep_kernel(const char* __restrict__ kc, const char* __restrict__ vc,
+                       const int* __restrict__ pos_ptr, int max_len, uint32_t* __restrict__ sink) {
+  const int L = min(pos_ptr[0] + 1, max_len);
+  const int s = blockIdx.x, g = blockIdx.y, GH = gridDim.x;
+  const uint64_t hb = (uint64_t)L * (HD * 2);  // < 2^32 - 32 KB (host check)
+  const uint64_t chunk = ((hb + GH - 1) / GH + 4095u) & ~4095ull;
+  if ((uint64_t)s * chunk >= hb) return;
+  const uint32_t beg = (uint32_t)(s * chunk);
+  const uint32_t end = (uint32_t)min((uint64_t)beg + chunk, hb);
+  const size_t head = (size_t)g * max_len * (HD * 2);
+  const __amdgpu_buffer_rsrc_t kr = make_rsrc_uniform(kc + head, end);
+  const __amdgpu_buffer_rsrc_t vr = make_rsrc_uniform(vc + head, end);
+  const uint32_t rounds = (end - beg + 4096u * DEPTH - 1) / (4096u * DEPTH);
+  uint32_t acc = 0;
+  for (uint32_t r = 0, off = beg + threadIdx.x * 16; r < rounds; ++r, off += 4096u * DEPTH) {
+    u32x4_t a[DEPTH], b[DEPTH];
+#pragma unroll
+    for (int j = 0; j < DEPTH; ++j) {
+      a[j] = buffer_load16_stream(kr, off + j * 4096);  // past the share's end: 0, no traffic
+      b[j] = buffer_load16_stream(vr, off + j * 4096);
+    }
+#pragma unroll
+    for (int j = 0; j < DEPTH; ++j) acc ^= a[j][0] ^ a[j][3] ^ b[j][0] ^ b[j][3];
+  }
+  if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
 __global__ void __launch_bounds__(WAVE) launch_probe_kernel() {}
 }  // namespace qe
 
 extern "C" hipError_t qe_kv_stream_probe(const void* kc, const void* vc, const int* pos, int Hkv,
                                          int max_len, int NS, void* sink, hipStream_t stream) {
   if (max_len < 1 || Hkv < 1 || NS < 1 || !kc || !vc || !pos || !sink ||
-      (unsigned long long)max_len * HD * 2 >= (1ull << 32))
+      (unsigned long long)(max_len + 64) * HD * 2 >= (1ull << 32))
     return hipErrorInvalidValue;
   kv_stream_probe_kernel<<<dim3(max_slices(max_len, NS), Hkv), dim3(256), 0, stream>>>(
       static_cast<const __bf16*>(kc), static_cast<const __bf16*>(vc), pos, max_len, ns_div(NS),
       static_cast<uint32_t*>(sink));
+  return hipGetLastError();
+}
+
+extern "C" hipError_t qe_kv_stream_sweep(const void* kc, const void* vc, const int* pos, int Hkv,
+                                         int max_len, int grid_per_head, int depth, void* sink,
+                                         hipStream_t stream) {
+  if (max_len < 1 || Hkv < 1 || grid_per_head < 1 || grid_per_head > 65535 || !kc || !vc ||
+      !pos || !sink || (unsigned long long)(max_len + 64) * HD * 2 >= (1ull << 32))
+    return hipErrorInvalidValue;
+  const dim3 grid(grid_per_head, Hkv);
+  const auto* K = static_cast<const char*>(kc);
+  const auto* V = static_cast<const char*>(vc);
+  auto* S = static_cast<uint32_t*>(sink);
+  switch (depth) {
+    case 4: kv_stream_sweep_kernel<4><<<grid, dim3(256), 0, stream>>>(K, V, pos, max_len, S); break;
+    case 8: kv_stream_sweep_kernel<8><<<grid, dim3(256), 0, stream>>>(K, V, pos, max_len, S); break;
+    case 16: kv_stream_sweep_kernel<16><<<grid, dim3(256), 0, stream>>>(K, V, pos, max_len, S); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -500,8 +500,9 @@ def test_layer_multi_row_passes_match_token_by_token(native):
 
 
 def test_measurement_probes_run(capi):
-    """The ceiling probes of the bench (measurement only) launch and return hipSuccess; the
-    stream probe's sink stays untouched (the folded value never hits the sentinel on N(0,1)
+    """The ceiling probes of the bench (measurement only: the stream probe on the partials grid
+    and the grid / depth sweep) launch and return hipSuccess; the stream probes' sink stays
+    untouched (the folded value never hits the sentinel on N(0,1)
     data), and an empty launch returns hipSuccess too."""
     L, hkv = 4096, 4
     g = torch.Generator(device=DEV).manual_seed(3)
@@ -511,6 +512,8 @@ def test_measurement_probes_run(capi):
     for p in (0, 100, L - 1, L + 50):
         pos = torch.tensor([p], dtype=torch.int32, device=DEV)
         assert capi.kv_stream_probe(kc, vc, pos, hkv, L, 64, sink) == 0
+        for gph, depth in ((1, 4), (64, 8), (512, 16), (4096, 4)):
+            assert capi.kv_stream_sweep(kc, vc, pos, hkv, L, gph, depth, sink) == 0
     assert capi.launch_probe() == 0
     torch.cuda.synchronize()
     assert int(sink.item()) == 0

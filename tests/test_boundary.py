@@ -91,6 +91,25 @@ def test_capi_decode_rejects(capi, kw, why):
     assert r == INVALID, why
 
 
+@pytest.mark.parametrize("max_len", [(1 << 23) - 64, (1 << 23) - 1, 0])
+def test_capi_stream_probes_reject_offsets_past_32_bits(capi, max_len):
+    """The measurement probes step 32-bit byte offsets up to 64 rows past the cache end: cache
+    lengths where that could wrap, (max_len + 64) * 512 >= 2^32, are rejected before any launch."""
+    lib = capi.load()
+    assert lib.qe_kv_stream_probe(A, A, A, 4, max_len, 16, A, None) == INVALID
+    assert lib.qe_kv_stream_sweep(A, A, A, 4, max_len, 64, 8, A, None) == INVALID
+
+
+@pytest.mark.parametrize("kw,why", [(dict(gph=0), "no workgroups"), (dict(gph=65536), "grid"),
+                                    (dict(depth=5), "depth"), (dict(hkv=0), "no heads"),
+                                    (dict(sink=None), "null sink")])
+def test_capi_stream_sweep_rejects(capi, kw, why):
+    a = dict(gph=64, depth=8, hkv=4, sink=A)
+    a.update(kw)
+    assert capi.load().qe_kv_stream_sweep(A, A, A, a["hkv"], 4096, a["gph"], a["depth"],
+                                          a["sink"], None) == INVALID, why
+
+
 @pytest.mark.parametrize("fp8", [False, True])
 @pytest.mark.parametrize("kw,why", [
     (dict(T=0), "no rows"), (dict(hq=25), "Hq % Hkv"), (dict(hkv=0), "no kv heads"),
