@@ -34,7 +34,7 @@ extern "C" {
  * Valid: 1 <= n <= 8, Hk >= 1, Hv % Hk == 0, Hv <= 65535, C < 2^26, ldp >= C, ldo >= Hv*128.
  * A call touches no memory but its arguments, so calls on different layers (different state,
  * ring, staging and output buffers) may run concurrently on any streams; calls that share those
- * buffers must be ordered, as in the reference. 4-8 rows run as two launches (each head split over
+ * buffers must be ordered, as in the reference. 5-8 rows run as two launches (each head split over
  * 4 workgroups, then a per-head finish); no workgroup waits for another.
  * Replaces launch_gdn_step_n (reference csrc/ops.h:20-23, csrc/gdn.cu:65-341). The reference's
  * thread-split argument `q` selects a CUDA block shape; it has no counterpart here. */

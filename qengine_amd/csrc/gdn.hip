@@ -13,12 +13,18 @@
 // pattern of calls with kept prefixes equals plain one-row decoding bit for bit.
 //
 // Two paths share the per-column arithmetic (gdn_common.hpp) and so give the same bits:
-// gdn_step_kernel (one workgroup per head, below) for 1-3 rows, and gdn_split_kernel (each head
-// over 4 workgroups) followed by gdn_finish_kernel (gdn_split.hip) for 4-8 rows.
+// gdn_step_kernel (one workgroup per head, below) for 1-4 rows, and gdn_split_kernel (each head
+// over 4 workgroups) followed by gdn_finish_kernel (gdn_split.hip) for 5-8 rows.
 //
-// gfx950 layout: one 512-thread workgroup (8 waves) per value head. Wave w owns state columns
-// 16w .. 16w+15; lane l holds rows 8(l>>2) .. +7 of columns 16w + 4(l&3) .. +3 (32 fp32 registers,
-// loaded as eight 16-byte rows). The dot products over the 128 state rows are a per-lane 8-term
+// gfx950 layout: one workgroup of NT = 1024 threads (16 waves, four per SIMD) per value head.
+// With NC = 2048 / NT state columns per lane, wave w owns columns 4 NC w .. +4 NC - 1 and lane l
+// holds rows 8(l>>2) .. +7 of columns 4 NC w + NC (l&3) .. +NC - 1 (16 fp32 registers at NC = 2,
+// loaded as eight 8-byte rows; NT = 512 gives NC = 4, 32 registers). Per delta-rule step the CU
+// runs the same 3 x 16,384 fp32 operations either way; 16 waves hide more of the butterflies'
+// and LDS latencies than 8 (same-box A/B on MI355X at Hk 16 / Hv 48, us per call at 1 / 2 / 3 /
+// 4 rows: 8.60 / 10.16 / 11.57 / 12.35 with 8 waves (the split path at 4) against 8.44 / 9.50 /
+// 10.70 / 12.03; at 6 and 8 rows the split path stays faster, 14.65 / 16.52 against 15.17 /
+// 18.05). The dot products over the 128 state rows are a per-lane 8-term
 // FMA chain followed by a butterfly over the 16 lanes that share a column quad (DPP xor 8 / 4,
 // permlane16 / 32 swaps), so the recurrence needs no LDS and no barrier. Each wave therefore holds
 // the whole column: kv, delta and o never leave the wave. Three barriers per call: after the
@@ -36,7 +42,8 @@
 
 namespace qe {
 
-__global__ void __launch_bounds__(GDN_THREADS)
+template <int NT>
+__global__ void __launch_bounds__(NT)
 gdn_step_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
                 const __bf16* __restrict__ b, const __bf16* __restrict__ a, long ldp,
                 __bf16* __restrict__ ring, const __bf16* __restrict__ conv_w,
@@ -50,8 +57,10 @@ gdn_step_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
   __shared__ __align__(16) float oa[GDN_MAXN][GDN_D];
   __shared__ float sg[GDN_MAXN][2], ga[GDN_MAXN][2], l2p[GDN_MAXN][4];
 
+  static_assert(NT == 512 || NT == 1024, "8 or 16 waves");
+  constexpr int NC = 2048 / NT;  // state columns per lane: 4 (8 waves) or 2 (16 waves)
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  const int rg = lane >> 2, col0 = 16 * w + 4 * (lane & 3);
+  const int rg = lane >> 2, col0 = 4 * NC * w + NC * (lane & 3);
   const int j = blockIdx.x, r = Hv / Hk, i = j / r;
   const int C = 2 * Hk * GDN_D + Hv * GDN_D;
   float* Sj = S + (size_t)j * GDN_D * GDN_D;
@@ -80,19 +89,18 @@ gdn_step_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
   __bf16 hb[3];  // x at positions P-3 .. P-1
 #pragma unroll
   for (int q = 0; q < 3; ++q) hb[q] = ring[(size_t)((P - 3 + q) & (GDN_RING - 1)) * C + chl];
-  const int srow = tid >> 6, su = tid & 63;  // staged rows: thread = (row, 16-byte piece of k or v)
+  // staged rows: thread = (row, 16-byte piece of k or v); waves 8-15 of the 16-wave kernel
+  // re-read row 7 and store nothing
+  const int srow = min(tid >> 6, GDN_MAXN - 1), su = tid & 63;
   const F4 stv = *reinterpret_cast<const F4*>(
       su < 32 ? st_k + ((size_t)srow * Hv + j) * GDN_D + 4 * su
               : st_v + ((size_t)srow * Hv + j) * GDN_D + 4 * (su - 32));
   const float2 stg = *reinterpret_cast<const float2*>(st_g + ((size_t)(tid & 7) * Hv + j) * 2);
-  float s[8][4];
-#pragma unroll
-  for (int rr = 0; rr < 8; ++rr) {
-    const F4 v = *reinterpret_cast<const F4*>(Sj + (size_t)(rg * 8 + rr) * GDN_D + col0);
-    s[rr][0] = v.x; s[rr][1] = v.y; s[rr][2] = v.z; s[rr][3] = v.w;
-  }
+  float s[8][NC];
+  load_state_rows(Sj, rg, col0, s);
 
-  *reinterpret_cast<F4*>(su < 32 ? &sk[srow][4 * su] : &sv[srow][4 * (su - 32)]) = stv;
+  if (tid < GDN_MAXN * 64)
+    *reinterpret_cast<F4*>(su < 32 ? &sk[srow][4 * su] : &sv[srow][4 * (su - 32)]) = stv;
   if (tid < GDN_MAXN) {
     sg[tid][0] = stg.x;
     sg[tid][1] = stg.y;
@@ -133,7 +141,7 @@ gdn_step_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
 
   // Stage this call's v and gates for the next call's replay. Only after the barrier: the staged
   // rows of the previous call (same addresses) have all been read into LDS by then.
-  for (int t = tid >> 7; t < n; t += GDN_THREADS / GDN_D)
+  for (int t = tid >> 7; t < n; t += NT / GDN_D)
     st_v[((size_t)t * Hv + j) * GDN_D + c] = va[t][c];
   if (tid < n)
     *reinterpret_cast<float2*>(st_g + ((size_t)tid * Hv + j) * 2) = make_float2(ga[tid][0], ga[tid][1]);
@@ -158,29 +166,24 @@ gdn_step_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
 
   // ---- 1. replay the rows kept by the previous call, write the committed state back ----
   for (int t = 0; t < pend; ++t) {
-    float k[8], v[4];
+    float k[8], v[NC];
     lds_read8(&sk[t][rg * 8], k);
-    lds_read4(&sv[t][col0], v);
+    vec_read_n(&sv[t][col0], v);
     delta_step(s, k, v, sg[t][0], sg[t][1]);
   }
-  if (pend > 0) {
-#pragma unroll
-    for (int rr = 0; rr < 8; ++rr)
-      *reinterpret_cast<F4*>(Sj + (size_t)(rg * 8 + rr) * GDN_D + col0) =
-          F4{s[rr][0], s[rr][1], s[rr][2], s[rr][3]};
-  }
+  if (pend > 0) store_state_rows(Sj, rg, col0, s);
   __syncthreads();
 
   // ---- 2. new rows on the register copy ----
   for (int t = 0; t < n; ++t) {
-    float k[8], q[8], v[4];
+    float k[8], q[8], v[NC];
     lds_read8(&ka[t][rg * 8], k);
     lds_read8(&qa[t][rg * 8], q);
-    lds_read4(&va[t][col0], v);
+    vec_read_n(&va[t][col0], v);
     delta_step(s, k, v, ga[t][0], ga[t][1]);
-    float o[4];
+    float o[NC];
     read_out(s, q, o);
-    if (rg == 0) *reinterpret_cast<F4*>(&oa[t][col0]) = F4{o[0], o[1], o[2], o[3]};
+    if (rg == 0) vec_write_n(&oa[t][col0], o);
   }
   __syncthreads();
 
@@ -208,11 +211,10 @@ extern "C" hipError_t qe_gdn_step_n(const void* qkv, const void* z, const void* 
   if (C >= (1L << 26) || ldp < C || ldo < (long)Hv * GDN_D) return hipErrorInvalidValue;
   if (!al(S, 16) || !al(st_k, 16) || !al(st_v, 16) || !al(st_g, 8) || !al(conv_w, 8))
     return hipErrorInvalidValue;
-  // 4-8 rows: the split kernel and its finish kernel; 1-3 rows: one workgroup per head (below
-  // four rows the split's second launch costs more than the spread saves: same-box A/B on
-  // MI355X at Hk 16 / Hv 48 with the split path under the max-ILP scheduler, 3 rows 11.60 vs
-  // 10.92 us, 4 rows 12.35 vs 12.67; earlier, 6 rows 15.4 vs 15.7 and 8 rows 17.4 vs 18.8).
-  // Both paths give the same bits.
+  // 5-8 rows: the split kernel and its finish kernel; 1-4 rows: one workgroup per head (below
+  // five rows the split's second launch costs more than the spread saves: same-box A/B on MI355X
+  // at Hk 16 / Hv 48, 4 rows 12.03 us one workgroup against 12.35 split; 6 rows 15.17 against
+  // 14.65). Both paths give the same bits.
   if (n >= GDN_SPLIT_MIN_ROWS)
     return launch_gdn_split(static_cast<const __bf16*>(qkv), static_cast<const __bf16*>(z),
                             static_cast<const __bf16*>(b), static_cast<const __bf16*>(a), ldp,
@@ -220,7 +222,7 @@ extern "C" hipError_t qe_gdn_step_n(const void* qkv, const void* z, const void* 
                             static_cast<const __bf16*>(A_log), static_cast<const __bf16*>(dt_bias),
                             static_cast<const __bf16*>(norm_w), S, st_k, st_v, st_g, ctl,
                             static_cast<__bf16*>(out), ldo, n, Hk, Hv, eps, stream);
-  gdn_step_kernel<<<dim3(Hv), dim3(GDN_THREADS), 0, stream>>>(
+  gdn_step_kernel<GDN_THREADS><<<dim3(Hv), dim3(GDN_THREADS), 0, stream>>>(
       static_cast<const __bf16*>(qkv), static_cast<const __bf16*>(z), static_cast<const __bf16*>(b),
       static_cast<const __bf16*>(a), ldp, static_cast<__bf16*>(ring),
       static_cast<const __bf16*>(conv_w), static_cast<const __bf16*>(A_log),

@@ -13,11 +13,11 @@ namespace qe {
 constexpr int GDN_D = 128;      // dk = dv
 constexpr int GDN_RING = 16;
 constexpr int GDN_MAXN = 8;
-constexpr int GDN_THREADS = 512;
+constexpr int GDN_THREADS = 1024;                   // one-workgroup kernel: 16 waves per head
 constexpr int GDN_SPLIT = 4;                        // workgroups per head in the split kernel
 constexpr int GDN_SPLIT_COLS = GDN_D / GDN_SPLIT;
 constexpr int GDN_SPLIT_THREADS = 512;
-constexpr int GDN_SPLIT_MIN_ROWS = 4;               // fewer rows: the one-workgroup kernel
+constexpr int GDN_SPLIT_MIN_ROWS = 5;               // fewer rows: the one-workgroup kernel
 
 struct __align__(16) F4 {
   float x, y, z, w;
@@ -101,6 +101,44 @@ __device__ __forceinline__ void lds_read4(const float* p, float (&d)[4]) {
   const F4 a = *reinterpret_cast<const F4*>(p);
   d[0] = a.x; d[1] = a.y; d[2] = a.z; d[3] = a.w;
 }
+// NC consecutive floats (NC = 1, 2 or 4), LDS or global memory: one vector access for 2 or 4.
+template <int NC>
+__device__ __forceinline__ void vec_read_n(const float* p, float (&d)[NC]) {
+  if constexpr (NC == 4) {
+    lds_read4(p, d);
+  } else if constexpr (NC == 2) {
+    const float2 a = *reinterpret_cast<const float2*>(p);
+    d[0] = a.x; d[1] = a.y;
+  } else {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) d[c] = p[c];
+  }
+}
+template <int NC>
+__device__ __forceinline__ void vec_write_n(float* p, const float (&d)[NC]) {
+  if constexpr (NC == 4) {
+    *reinterpret_cast<F4*>(p) = F4{d[0], d[1], d[2], d[3]};
+  } else if constexpr (NC == 2) {
+    *reinterpret_cast<float2*>(p) = make_float2(d[0], d[1]);
+  } else {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) p[c] = d[c];
+  }
+}
+// This lane's block of a head's state (rows 8 rg .. +7, columns col0 .. col0 + NC - 1 of the
+// row-major [128][128] fp32 state): 8 loads of 4 NC bytes, and the write-back.
+template <int NC>
+__device__ __forceinline__ void load_state_rows(const float* Sj, int rg, int col0,
+                                                float (&s)[8][NC]) {
+#pragma unroll
+  for (int rr = 0; rr < 8; ++rr) vec_read_n(Sj + (size_t)(rg * 8 + rr) * GDN_D + col0, s[rr]);
+}
+template <int NC>
+__device__ __forceinline__ void store_state_rows(float* Sj, int rg, int col0,
+                                                 const float (&s)[8][NC]) {
+#pragma unroll
+  for (int rr = 0; rr < 8; ++rr) vec_write_n(Sj + (size_t)(rg * 8 + rr) * GDN_D + col0, s[rr]);
+}
 
 // Gated RMSNorm of one output row of a head (wave-wide; lane holds columns 2 lane, 2 lane + 1):
 // out = bf16(bf16(w * bf16(o * r)) * silu(z)), r = 1 / sqrt(sum(o^2) / 128 + eps). The sum of
@@ -128,7 +166,7 @@ __device__ __forceinline__ void gated_norm_row(const float* __restrict__ o_row, 
   op[2 * lane + 1] = f32_to_bf16(y1 * silu_f(z1));
 }
 
-// Split path for 4-8 rows (gdn_split.hip): gdn_split_kernel then gdn_finish_kernel.
+// Split path for 5-8 rows (gdn_split.hip): gdn_split_kernel then gdn_finish_kernel.
 hipError_t launch_gdn_split(const __bf16* qkv, const __bf16* z, const __bf16* b, const __bf16* a,
                             long ldp, __bf16* ring, const __bf16* conv_w, const __bf16* A_log,
                             const __bf16* dt_bias, const __bf16* norm_w, float* S, float* st_k,

@@ -1,4 +1,4 @@
-// Gated DeltaNet step, split path for 4-8 rows: gdn_split_kernel (each value head's 128 state
+// Gated DeltaNet step, split path for 5-8 rows: gdn_split_kernel (each value head's 128 state
 // columns over 4 workgroups) followed by gdn_finish_kernel (one workgroup per head). Same
 // per-column arithmetic as gdn_step_kernel (gdn.hip), so the same bits.
 //
