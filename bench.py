@@ -537,7 +537,8 @@ def bench_gemv(torch, C, qa, steps: int, warmup: int) -> dict:
             gbps = wbytes / (us * 1e3)
             res[f"{name}_rows{nr}"] = {"us": round(us, 3), "GBps": round(gbps, 1),
                                        "hbm_frac": round(gbps / HBM_PEAK_GBS, 4),
-                                       "kparts": capi.gemv_kparts(N, K)}
+                                       "kparts": capi.gemv_kparts(N, K),
+                                       "tile_rows": capi.gemv_tile_rows(N, K)}
         del Ws
     nbytes = 2 * 2 ** 30
     buf = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)

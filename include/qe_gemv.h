@@ -28,6 +28,13 @@ hipError_t qe_gemv_bf16(const void* W, const void* x, void* out, int nr, int N, 
  * the partial sums of a tile are added in order 0..parts-1. No counterpart in the reference. */
 int qe_gemv_kparts(int N, int K);
 
+/* Rows of W per tile qe_gemv_bf16 uses for an [N][K] weight on the current device (16, 14, 12
+ * or 10; 0 if invalid): 16 unless the grid has one tile per workgroup (4 k-parts) and at most 4
+ * workgroups per compute unit, then the height whose grid best fills its last round over the
+ * compute units (5120 x 6144: 10, 512 workgroups; 14336 x 5120: 14, 1024 workgroups on 256
+ * CUs). Outputs do not depend on it bit for bit. No counterpart in the reference. */
+int qe_gemv_tile_rows(int N, int K);
+
 /* Reads `bytes` (a multiple of 16) from 16-byte aligned device memory `buf` once with 16-byte
  * non-temporal loads, one contiguous range per workgroup over 2048 workgroups, to measure
  * achievable streaming-read bandwidth;

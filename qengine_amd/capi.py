@@ -44,6 +44,7 @@ SIGNATURES = {
     "qe_attn_decode_fp8_partials": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P]),
     "qe_gemv_bf16": (_I, [_P, _P, _P, _I, _I, _I, _L, _L, _P]),
     "qe_gemv_kparts": (_I, [_I, _I]),
+    "qe_gemv_tile_rows": (_I, [_I, _I]),
     "qe_hbm_read_probe": (_I, [_P, ctypes.c_size_t, _P, _P]),
     "qe_embed": (_I, [_P, _P, _P, _I, _I, _I, _L, _P]),
     "qe_rmsnorm1p": (_I, [_P, _P, _P, _P, _I, _I, _L, _L, _L, _F, _P]),
@@ -184,6 +185,10 @@ def gemv_bf16(W, x, out, nr, N, K, ldx, ldo, stream=None) -> int:
 
 def gemv_kparts(N: int, K: int) -> int:
     return load().qe_gemv_kparts(N, K)
+
+
+def gemv_tile_rows(N: int, K: int) -> int:
+    return load().qe_gemv_tile_rows(N, K)
 
 
 def hbm_read_probe(buf, nbytes: int, sink, stream=None) -> int:

@@ -25,8 +25,15 @@
 //  * A workgroup holds 4 waves = 4/S row tiles x S k-parts; S grows as N shrinks so small
 //    projections still keep the CUs streaming. The S partial sums are added through LDS in the
 //    fixed order 0..S-1, so results never depend on timing.
+//  * A tile is 16 rows of W unless a grid of 16-row tiles would leave the CUs' last round of
+//    workgroups part-empty: then it is re-cut into tiles of 14, 12 or 10 rows that fill it
+//    (qe_gemv_tile_rows; o_proj 5120 x 6144: 320 workgroups of 16 rows -> 512 of 10, two per
+//    CU, 13.50 -> 11.79 us at 1 row and 15.55 -> 13.39 us at 5 rows on MI355X). An output's
+//    arithmetic does not depend on its row's place in a tile, so the bits do not change.
 #include "gemv_common.hpp"
 #include "qe_gemv.h"
+
+#include <atomic>
 
 namespace qe {
 
@@ -37,36 +44,37 @@ namespace qe {
 // workgroups fit on a CU at any row count (with the rows in LDS, 3-8 rows took 88-104 KB and
 // one workgroup per CU). The MFMA operands are the same bits, so results are identical to the
 // LDS-staged kernel's. Two ring stages with their register sets are unrolled as a pair.
-template <int S>
+template <int S, int RPT>
 __global__ void __launch_bounds__(GEMV_WAVES * WAVE)
 gemv_bf16_xr_kernel(const __bf16* __restrict__ W, const __bf16* __restrict__ x,
                     __bf16* __restrict__ out, int nr, int N, int K, long ldx, long ldo) {
   constexpr int RT = GEMV_WAVES / S;
-  constexpr int SLOTS = GEMV_W_SLOTS;
-  constexpr int LPS = GEMV_W_SLOTS / 64 + GEMV_KB / 32;  // loads per stage: 8 W DMA + 8 x
+  constexpr int SLOTS = gemv_w_slots<RPT>();
+  constexpr int LPS = RPT / 2 + GEMV_KB / 32;  // loads per stage: RPT / 2 W DMA + 8 x
   extern __shared__ __attribute__((aligned(16))) u32x4_t gemv_smem[];
   const int lane = threadIdx.x & (WAVE - 1);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   const int i = lane & 15, g4 = lane >> 4;
   const int tile = blockIdx.x * RT + w / S, kp = w % S;
-  const int r0 = tile * 16;
+  const int r0 = tile * RPT;
   const bool live = r0 < N;
 
   const int K8 = K >> 3;
   const int nblk = (K + GEMV_KB - 1) / GEMV_KB;
   const int b_beg = kp * nblk / S, b_end = live ? (kp + 1) * nblk / S : b_beg;
-  const uint32_t tile_bytes = live ? (uint32_t)min(16, N - r0) * (uint32_t)K * 2u : 0u;
+  const uint32_t tile_bytes = live ? (uint32_t)min(RPT, N - r0) * (uint32_t)K * 2u : 0u;
   const __amdgpu_buffer_rsrc_t wrs = make_rsrc_uniform(W + (size_t)r0 * K, tile_bytes);
   const __amdgpu_buffer_rsrc_t xrs =
       make_rsrc_uniform(x, (uint32_t)(((size_t)(nr - 1) * ldx + K) * 2));
   u32x4_t* ring = gemv_smem + (size_t)w * GEMV_STG * SLOTS;
   const int cr = i < nr ? i : nr - 1;  // the activation row this lane's column reads
   const bool xok = i < nr;
+  const bool aok = RPT == 16 || i < RPT;  // this lane's W row is part of the tile
 
   auto issue = [&](int blk, int st, u32x4_t (&xv)[GEMV_KB / 32]) __attribute__((always_inline)) {
     u32x4_t* sb = ring + st * SLOTS;
 #pragma unroll
-    for (int j = 0; j < GEMV_W_SLOTS / 64; ++j) {
+    for (int j = 0; j < RPT / 2; ++j) {
       const int r = 2 * j + (lane >> 5), q = lane & 31;
       buffer_load16_to_lds(wrs, (uint32_t)r * (uint32_t)K * 2u +
                                     (uint32_t)(blk * GEMV_KB + (q ^ (r & 15)) * 8) * 2u,
@@ -87,8 +95,8 @@ gemv_bf16_xr_kernel(const __bf16* __restrict__ W, const __bf16* __restrict__ x,
       const int q = 4 * ks + g4;
       const bool ok = cbase + q < K8;
       const u32x4_t z = {0u, 0u, 0u, 0u};
-      const u32x4_t a = sb[i * 32 + (q ^ i)];
-      acc = mfma16x16x32(as_bf16x8(ok ? a : z), as_bf16x8(ok && xok ? xv[ks] : z), acc);
+      const u32x4_t a = sb[(aok ? i : 0) * 32 + (q ^ i)];
+      acc = mfma16x16x32(as_bf16x8(ok && aok ? a : z), as_bf16x8(ok && xok ? xv[ks] : z), acc);
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -129,7 +137,7 @@ gemv_bf16_xr_kernel(const __bf16* __restrict__ W, const __bf16* __restrict__ x,
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int row = r0 + 4 * g4 + j;
-      if (row < N) op[row] = f32_to_bf16(acc[j]);
+      if (4 * g4 + j < RPT && row < N) op[row] = f32_to_bf16(acc[j]);
     }
   }
 }
@@ -159,19 +167,34 @@ hbm_read_probe_kernel(const u32x4_t* __restrict__ p, size_t n16, uint32_t* __res
   if (acc == 0x9E3779B9u) sink[0] = acc;
 }
 
-template <int S>
+template <int S, int RPT>
 static hipError_t launch_gemv_xr(const __bf16* W, const __bf16* x, __bf16* out, int nr, int N,
                                  int K, long ldx, long ldo, hipStream_t stream) {
   constexpr int RT = GEMV_WAVES / S;
-  constexpr size_t lds = (size_t)GEMV_WAVES * GEMV_STG * GEMV_W_SLOTS * 16;
+  constexpr size_t lds = (size_t)GEMV_WAVES * GEMV_STG * gemv_w_slots<RPT>() * 16;
   static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_bf16_xr_kernel<S>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_bf16_xr_kernel<S, RPT>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (attr != hipSuccess) return attr;
-  const int tiles = (N + 15) / 16;
-  gemv_bf16_xr_kernel<S><<<dim3((tiles + RT - 1) / RT), dim3(GEMV_WAVES * WAVE), lds, stream>>>(
+  const int tiles = (N + RPT - 1) / RPT;
+  gemv_bf16_xr_kernel<S, RPT><<<dim3((tiles + RT - 1) / RT), dim3(GEMV_WAVES * WAVE), lds, stream>>>(
       W, x, out, nr, N, K, ldx, ldo);
   return hipGetLastError();
+}
+
+// Compute units of the current device (256 on MI355X; 256 when it cannot be queried).
+static int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int c = cache[dev].load(std::memory_order_relaxed);
+  if (c == 0) {
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        c < 1)
+      c = 256;
+    cache[dev].store(c, std::memory_order_relaxed);
+  }
+  return c;
 }
 
 }  // namespace qe
@@ -190,6 +213,26 @@ extern "C" int qe_gemv_kparts(int N, int K) {
   return S;
 }
 
+extern "C" int qe_gemv_tile_rows(int N, int K) {
+  if (N < 1 || K < 1) return 0;
+  // Only grids of one tile per workgroup (S = 4) and at most 4 workgroups per CU are re-cut:
+  // with more rounds the part-empty last one is a small share of the call.
+  const long cus = device_cus();
+  if (qe_gemv_kparts(N, K) != 4 || (N + 15) / 16 > 4 * cus) return 16;
+  // the tile height whose grid best fills its last round over the CUs; ties keep taller tiles
+  int best = 16;
+  long best_w = 0, best_slots = 1;
+  for (int r : {16, 14, 12, 10}) {
+    const long w = (N + r - 1) / r, slots = (w + cus - 1) / cus * cus;
+    if (w * best_slots > best_w * slots) {  // w / slots > best_w / best_slots
+      best = r;
+      best_w = w;
+      best_slots = slots;
+    }
+  }
+  return best;
+}
+
 extern "C" hipError_t qe_gemv_bf16(const void* W, const void* x, void* out, int nr, int N, int K,
                                    long ldx, long ldo, hipStream_t stream) {
   if (nr < 1 || nr > 8 || N < 1 || K < 8 || K % 8 != 0 || ldx < K || ldo < N || !W || !x ||
@@ -206,14 +249,21 @@ extern "C" hipError_t qe_gemv_bf16(const void* W, const void* x, void* out, int 
   const auto* xb = static_cast<const __bf16*>(x);
   auto* ob = static_cast<__bf16*>(out);
   const int S = qe_gemv_kparts(N, K);
+  const int RPT = qe_gemv_tile_rows(N, K);  // below 16 only with S = 4
   if (nr >= 3) {  // activation rows in registers: two workgroups per CU at any row count
     switch (S) {
-      case 1: return launch_gemv_xr<1>(Wb, xb, ob, nr, N, K, ldx, ldo, stream);
-      case 2: return launch_gemv_xr<2>(Wb, xb, ob, nr, N, K, ldx, ldo, stream);
-      default: return launch_gemv_xr<4>(Wb, xb, ob, nr, N, K, ldx, ldo, stream);
+      case 1: return launch_gemv_xr<1, 16>(Wb, xb, ob, nr, N, K, ldx, ldo, stream);
+      case 2: return launch_gemv_xr<2, 16>(Wb, xb, ob, nr, N, K, ldx, ldo, stream);
+      default:
+        switch (RPT) {
+          case 10: return launch_gemv_xr<4, 10>(Wb, xb, ob, nr, N, K, ldx, ldo, stream);
+          case 12: return launch_gemv_xr<4, 12>(Wb, xb, ob, nr, N, K, ldx, ldo, stream);
+          case 14: return launch_gemv_xr<4, 14>(Wb, xb, ob, nr, N, K, ldx, ldo, stream);
+          default: return launch_gemv_xr<4, 16>(Wb, xb, ob, nr, N, K, ldx, ldo, stream);
+        }
     }
   }
-  return launch_gemv_lds(S, (nr + 1) / 2, Wb, xb, ob, nr, N, K, ldx, ldo, stream);
+  return launch_gemv_lds(S, (nr + 1) / 2, RPT, Wb, xb, ob, nr, N, K, ldx, ldo, stream);
 }
 
 extern "C" hipError_t qe_hbm_read_probe(const void* buf, size_t bytes, void* sink,

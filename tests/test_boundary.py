@@ -29,7 +29,7 @@ def test_header_declares_the_path():
     syms = declared_symbols()
     for s in ("qe_attn_prep", "qe_attn_decode", "qe_attn_decode_partials",
               "qe_attn_decode_combine", "qe_attn_split_size", "qe_attn_version", "qe_gemv_bf16",
-              "qe_gemv_kparts", "qe_hbm_read_probe"):
+              "qe_gemv_kparts", "qe_gemv_tile_rows", "qe_hbm_read_probe"):
         assert s in syms
 
 
@@ -386,6 +386,24 @@ def test_gemv_kparts():
     assert capi.gemv_kparts(5120, 1024) == 2
     assert capi.gemv_kparts(7, 64) == 1
     assert capi.gemv_kparts(0, 64) == 0
+
+
+def test_gemv_tile_rows():
+    """Rows per W tile: 16 unless a one-tile-per-workgroup grid of at most 4 workgroups per CU
+    leaves the last round part-empty; then the height that fills it best (no GPU here: 256 CUs
+    assumed, MI355X's count)."""
+    import qengine_amd.capi as capi
+    assert capi.gemv_tile_rows(5120, 6144) == 10     # o_proj: 320 -> 512 workgroups
+    assert capi.gemv_tile_rows(14336, 5120) == 14    # in_proj: 896 -> 1024 workgroups
+    assert capi.gemv_tile_rows(4096, 6144) == 16     # 256 workgroups already fill the CUs
+    assert capi.gemv_tile_rows(248320, 5120) == 16   # lm_head: 1 k-part, 16 rounds
+    assert capi.gemv_tile_rows(40000, 5120) == 16    # 2 k-parts
+    assert capi.gemv_tile_rows(16400, 5120) == 16    # 1,025 tiles: more than 4 per CU
+    assert capi.gemv_tile_rows(1000, 1024) == 16     # 2 k-parts (4 blocks of 256 k)
+    assert capi.gemv_tile_rows(1000, 2048) == 10     # 63 -> 100 workgroups
+    assert capi.gemv_tile_rows(7, 64) == 16
+    assert capi.gemv_tile_rows(0, 64) == 0
+    assert capi.gemv_tile_rows(64, 0) == 0
 
 
 def test_gemv_contract(native):

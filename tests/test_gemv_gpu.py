@@ -71,6 +71,29 @@ def test_gemv_rows_bit_exact(native, nr, N, K):
         assert torch.equal(out[r], one), r
 
 
+@pytest.mark.parametrize("nr", [1, 2, 5, 8])
+def test_gemv_tile_height_keeps_bits(native, capi, nr):
+    """Row prefixes of one weight cut into tiles of 10, 16, 14 and 12 rows (qe_gemv_tile_rows on
+    256 CUs) give the same bits for every shared row: an output does not depend on its row's
+    place in a tile. Both kernels (1-2 rows LDS-staged, 3-8 rows register activations)."""
+    K = 2048
+    g = torch.Generator(device=DEV).manual_seed(31 + nr)
+    W = torch.randn(5120, K, device=DEV, generator=g).to(BF)
+    x = torch.randn(nr, K, device=DEV, generator=g).to(BF)
+    full = torch.empty(nr, 5120, dtype=BF, device=DEV)
+    native.gemv_bf16(W, x, full)
+    heights = {}
+    for N in (5120, 4096, 3584, 3072, 2560, 1000):
+        heights[N] = capi.gemv_tile_rows(N, K)
+        assert capi.gemv_kparts(N, K) == 4
+        out = torch.empty(nr, N, dtype=BF, device=DEV)
+        native.gemv_bf16(W[:N], x, out)
+        assert torch.equal(out, full[:, :N]), (N, heights[N])
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert heights == {5120: 10, 4096: 16, 3584: 14, 3072: 12, 2560: 10, 1000: 10}
+    _check(full.cpu(), W.cpu(), x.cpu())
+
+
 @pytest.mark.parametrize("nr", [1, 3, 6, 8])
 @pytest.mark.parametrize("N,K", [(100, 8), (300, 264), (64, 520), (2000, 4104)])
 def test_gemv_partial_k_blocks(native, nr, N, K):
