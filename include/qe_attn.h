@@ -44,8 +44,11 @@ hipError_t qe_attn_prep(const void* qg, const void* k, const void* v, long ldp, 
  * Two launches: split-KV partials, row t over slices of qe_attn_split_size(L_t, NS) positions
  * (L_t = min(pos+t+1, max_len), so about NS slices hold work whatever max_len is), then a
  * log-sum-exp combine with the fused sigmoid gate. Row t of an n-row call is bit-identical to a
- * 1-row call at position pos+t. Valid: 1 <= n <= 8, Hq % Hkv == 0,
- * (Hq/Hkv)*n <= 64, NS >= 1, (max_len+32)*512 < 2^32, 16-byte aligned q/kc/vc/part_o.
+ * 1-row call at position pos+t. Valid: 1 <= n <= 65535, Hq % Hkv == 0 (any group size),
+ * NS >= 1, (max_len+32)*512 < 2^32, 16-byte aligned q/kc/vc/part_o. A call whose query
+ * columns ((Hq/Hkv)*n) exceed one launch's 64 runs the partials as several launches (chunks of
+ * min(8, 64/(Hq/Hkv)) rows; above 64 q heads per KV head, one row and at most 64 of its q heads
+ * per launch), with the same bits.
  * Replaces launch_attn_decode (reference csrc/ops.h:28-30, csrc/attn.cu:165-172). */
 hipError_t qe_attn_decode(const void* q, const void* kc, const void* vc, const int* pos,
                           const void* qg, long ldp, float* part_o, float* part_ml, void* out,
@@ -55,8 +58,8 @@ hipError_t qe_attn_decode(const void* q, const void* kc, const void* vc, const i
 /* qe_attn_prep followed by qe_attn_decode (same arguments; q_out is also the decode's q), in two
  * launches instead of three: the split-KV kernel computes its q rows and writes the new K/V
  * cache rows itself, then the combine runs. Every output (q_out, the written cache rows, out) is
- * bit-identical to the two calls in sequence. Valid: the union of both ops' ranges (1 <= n <= 8,
- * (Hq/Hkv)*n <= 64, ...); shapes wider than 16 columns ((Hq/Hkv)*n > 16) run the two ops.
+ * bit-identical to the two calls in sequence. Valid: the union of both ops' ranges (1 <= n <=
+ * 65535, ...); more than 8 rows or 16 columns ((Hq/Hkv)*n > 16) run the two ops.
  * No counterpart in the reference, which overlaps the two launches with programmatic dependent
  * launch instead (csrc/attn.cu:155, csrc/common.cuh:12-46; callers python/qengine/engine.py:455-458). */
 hipError_t qe_attn_prep_decode(const void* qg, const void* k, const void* v, long ldp,

@@ -27,6 +27,7 @@
 //    moved (an exact no-op).
 //  * Buffer resources bound the K/V reads to the slice: positions past it load as 0.
 //  * A second launch merges the slices (log-sum-exp) and applies the sigmoid gate.
+#include <algorithm>
 #include <mutex>
 #include <utility>
 
@@ -578,8 +579,8 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
 attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf16* vc,
                      const int* __restrict__ pos_ptr, float* __restrict__ part_o,
                      float* __restrict__ part_ml, int n, int Hq, int Hkv, int max_len, int NS,
-                     NsDiv nd, float scale_log2, PrepIn pin) {
-  const int pos0 = pos_ptr[0];  // first: the slicing waits for it
+                     NsDiv nd, float scale_log2, PrepIn pin, int row0) {
+  const int pos0 = pos_ptr[0] + row0;  // first: the slicing waits for it
   const int s = blockIdx.x, g = blockIdx.y;
   const int grp = Hq / Hkv;
   // The wave index as a wave-uniform value, so that tile positions and the addresses derived
@@ -1031,11 +1032,11 @@ __global__ void __launch_bounds__(cols::SUBSETS * (NT / CPW) * WAVE)
 attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ kc,
                           const __bf16* __restrict__ vc, const int* __restrict__ pos_ptr,
                           float* __restrict__ part_o, float* __restrict__ part_ml, int n, int Hq,
-                          int Hkv, int max_len, int NS, NsDiv nd, float scale_log2) {
+                          int Hkv, int max_len, int NS, NsDiv nd, float scale_log2, int row0) {
   static_assert(NT % CPW == 0, "column tiles split evenly over the waves of a subset");
   constexpr int SUB = cols::SUBSETS;
   constexpr int WPS = NT / CPW;  // waves per subset
-  const int pos0 = pos_ptr[0];  // first: the slicing waits for it
+  const int pos0 = pos_ptr[0] + row0;  // first: the slicing waits for it
   const int s = blockIdx.x, g = blockIdx.y;
   const int grp = Hq / Hkv;
   const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
@@ -1350,21 +1351,22 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 static hipError_t check_decode_shape(int n, int Hq, int Hkv, int max_len, int NS) {
-  if (n < 1 || n > 8 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || NS < 1 || max_len < 1)
+  if (n < 1 || n > MAX_DECODE_ROWS || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || NS < 1 ||
+      max_len < 1)
     return hipErrorInvalidValue;
-  if ((Hq / Hkv) * n > 64) return hipErrorInvalidValue;            // at most 4 column tiles
   // byte offsets of the last tile (up to one tile past max_len) must fit the 32-bit buffer range
   if ((unsigned long long)(max_len + TILE) * HD * 2 >= (1ull << 32))
     return hipErrorInvalidValue;
   return hipSuccess;
 }
 
-// kv8: the cache is the fp8 KV format; k_scale multiplies every score (q . (code * k_scale)),
-// folded into the softmax scale.
-static hipError_t launch_partials(const void* q, const void* kc, const void* vc, const int* pos,
-                                  float* part_o, float* part_ml, int n, int Hq, int Hkv,
-                                  int max_len, int NS, float scale, hipStream_t stream,
-                                  bool kv8 = false, float k_scale = 1.f) {
+// One launch of the partials kernels: n <= 8 rows and at most 64 query columns per workgroup
+// ((Hq/Hkv) n <= 64, 4 tiles of 16), the first row at position pos[0] + row0. kv8: the cache is the fp8 KV format; k_scale multiplies
+// every score (q . (code * k_scale)), folded into the softmax scale.
+static hipError_t launch_partials_tiles(const void* q, const void* kc, const void* vc,
+                                        const int* pos, float* part_o, float* part_ml, int n,
+                                        int Hq, int Hkv, int max_len, int NS, float scale,
+                                        hipStream_t stream, bool kv8, float k_scale, int row0) {
   const dim3 grid(max_slices(max_len, NS), Hkv);
   const NsDiv nd = ns_div(NS);
   const float scale_log2 = scale * 1.4426950408889634f * k_scale;
@@ -1374,15 +1376,15 @@ static hipError_t launch_partials(const void* q, const void* kc, const void* vc,
   const auto* V = static_cast<const __bf16*>(vc);
   if (kv8) {
     if (NT == 1 && n == 1)
-      attn_partials_kernel<1, false, false, true><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{});
+      attn_partials_kernel<1, false, false, true><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{}, row0);
     else if (NT == 1)
-      attn_partials_kernel<1, false, true, true><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{});
+      attn_partials_kernel<1, false, true, true><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{}, row0);
     else if (NT == 2)
-      attn_partials_kernel<2, false, true, true><<<grid, dim3(waves_for<2>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{});
+      attn_partials_kernel<2, false, true, true><<<grid, dim3(waves_for<2>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{}, row0);
     else if (NT == 3)
-      attn_partials_cols_kernel<3, 1, true><<<grid, dim3(cols::SUBSETS * 3 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2);
+      attn_partials_cols_kernel<3, 1, true><<<grid, dim3(cols::SUBSETS * 3 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, row0);
     else
-      attn_partials_cols_kernel<4, 2, true><<<grid, dim3(cols::SUBSETS * 2 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2);
+      attn_partials_cols_kernel<4, 2, true><<<grid, dim3(cols::SUBSETS * 2 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, row0);
     return hipGetLastError();
   }
   // NT = 1, 2: every wave holds all column tiles (measured fastest at 1-5 rows, GQA 6), except
@@ -1392,21 +1394,63 @@ static hipError_t launch_partials(const void* q, const void* kc, const void* vc,
   // The two give the same bits per column.
   // NT = 3, 4: one subset wave per column tile (the one-tile kernel would spill: 2.3-2.8x slower).
   if (NT == 2 && split_size(max_len, nd) <= 4 * TILE) {
-    attn_partials_cols_kernel<2, 1><<<grid, dim3(cols::SUBSETS * 2 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2);
+    attn_partials_cols_kernel<2, 1><<<grid, dim3(cols::SUBSETS * 2 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, row0);
     return hipGetLastError();
   }
   switch (NT) {
     case 1:
       if (n == 1)
-        attn_partials_kernel<1, false, false><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{});
+        attn_partials_kernel<1, false, false><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{}, row0);
       else
-        attn_partials_kernel<1><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{});
+        attn_partials_kernel<1><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{}, row0);
       break;
-    case 2: attn_partials_kernel<2><<<grid, dim3(waves_for<2>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{}); break;
-    case 3: attn_partials_cols_kernel<3, 1><<<grid, dim3(cols::SUBSETS * 3 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2); break;
-    default: attn_partials_cols_kernel<4, 2><<<grid, dim3(cols::SUBSETS * 2 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2); break;
+    case 2: attn_partials_kernel<2><<<grid, dim3(waves_for<2>() * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, PrepIn{}, row0); break;
+    case 3: attn_partials_cols_kernel<3, 1><<<grid, dim3(cols::SUBSETS * 3 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, row0); break;
+    default: attn_partials_cols_kernel<4, 2><<<grid, dim3(cols::SUBSETS * 2 * WAVE), 0, stream>>>(Q, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, row0); break;
   }
   return hipGetLastError();
+}
+
+// Any row count and group size, as several launches of the kernels above when one launch's 64
+// query columns do not hold the call. Rows are independent (row t attends up to position
+// pos[0] + t, reads q[t] and writes part_o[t], part_ml[t]), so a chunk of rows starting at row
+// r0 is the same call on offset q / part_o / part_ml pointers with row0 = r0. Up to 64 q
+// heads per KV head (G = Hq/Hkv), chunks of min(8, 64/G) rows. Beyond that, one row per launch
+// and each KV head's q heads in ceil(G/64) sub-groups of consecutive heads, each launched as a
+// one-KV-head call (Hkv = 1) on that head's cache and the sub-group's q, part_o and part_ml
+// heads. A column's arithmetic does not depend on how many columns its launch holds, so every
+// row of every shape has the bits of a 1-row call.
+static hipError_t launch_partials(const void* q, const void* kc, const void* vc, const int* pos,
+                                  float* part_o, float* part_ml, int n, int Hq, int Hkv,
+                                  int max_len, int NS, float scale, hipStream_t stream,
+                                  bool kv8 = false, float k_scale = 1.f) {
+  const int G = Hq / Hkv;
+  const auto* Q = static_cast<const __bf16*>(q);
+  if (G <= 64) {
+    const int chunk = std::min(8, 64 / G);
+    for (int r0 = 0; r0 < n; r0 += chunk) {
+      const size_t heads = (size_t)r0 * Hq;
+      const hipError_t e = launch_partials_tiles(
+          Q + heads * HD, kc, vc, pos, part_o + heads * NS * HD, part_ml + heads * NS * 2,
+          std::min(chunk, n - r0), Hq, Hkv, max_len, NS, scale, stream, kv8, k_scale, r0);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
+  const int SG = (G + 63) / 64;                     // sub-groups per KV head
+  const size_t kv_head = (size_t)max_len * HD * (kv8 ? 1 : 2);  // cache bytes per KV head
+  for (int t = 0; t < n; ++t)
+    for (int g = 0; g < Hkv; ++g)
+      for (int u = 0; u < SG; ++u) {
+        const int h0 = g * G + u * G / SG, h1 = g * G + (u + 1) * G / SG;
+        const size_t head = (size_t)t * Hq + h0;
+        const hipError_t e = launch_partials_tiles(
+            Q + head * HD, static_cast<const char*>(kc) + g * kv_head,
+            static_cast<const char*>(vc) + g * kv_head, pos, part_o + head * NS * HD,
+            part_ml + head * NS * 2, 1, h1 - h0, 1, max_len, NS, scale, stream, kv8, k_scale, t);
+        if (e != hipSuccess) return e;
+      }
+  return hipSuccess;
 }
 
 }  // namespace qe
@@ -1433,8 +1477,8 @@ extern "C" hipError_t qe_attn_decode_combine(const float* part_o, const float* p
                                              const int* pos, const void* qg, long ldp, void* out,
                                              long ldo, int n, int Hq, int max_len, int NS,
                                              hipStream_t stream) {
-  if (n < 1 || n > 8 || Hq < 1 || NS < 1 || max_len < 1 || !part_o || !part_ml || !pos || !qg ||
-      !out)
+  if (n < 1 || n > MAX_DECODE_ROWS || Hq < 1 || NS < 1 || max_len < 1 || !part_o || !part_ml ||
+      !pos || !qg || !out)
     return hipErrorInvalidValue;
   return launch_combine(part_o, part_ml, pos, qg, ldp, out, ldo, n, Hq, max_len, NS, stream);
 }
@@ -1553,7 +1597,7 @@ extern "C" hipError_t qe_attn_prep_decode(const void* qg, const void* k, const v
   // a multiple of 8 dims, and input rows the 16-byte loads cannot read: the prep kernel, then the
   // decode. (Two column tiles fused, 3-5 rows at GQA 6, measured slower than the two ops: 25.9
   // against 18.9 us per layer-call at 5 rows on a 4k cache, same bits.)
-  if (NT > 1 || rd == 0 || rd % 8 != 0 || n * (rd / 2) > ROPE_TAB || ldp % 8 != 0 ||
+  if (NT > 1 || n > 8 || rd == 0 || rd % 8 != 0 || n * (rd / 2) > ROPE_TAB || ldp % 8 != 0 ||
       !aligned16(qg) || !aligned16(k) || !aligned16(qnw) || !aligned16(knw) ||
       !aligned16(inv_freq)) {
     e = qe_attn_prep(qg, k, v, ldp, qnw, knw, inv_freq, pos, q_out, kc, vc, n, Hq, Hkv, max_len,
@@ -1573,10 +1617,10 @@ extern "C" hipError_t qe_attn_prep_decode(const void* qg, const void* k, const v
   const auto* V = static_cast<const __bf16*>(vc);
   if (n == 1)
     attn_partials_kernel<1, true, false><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(
-        nullptr, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, pin);
+        nullptr, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, pin, 0);
   else
     attn_partials_kernel<1, true><<<grid, dim3(waves_for<1>() * WAVE), 0, stream>>>(
-        nullptr, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, pin);
+        nullptr, K, V, pos, part_o, part_ml, n, Hq, Hkv, max_len, NS, nd, scale_log2, pin, 0);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   return qe_attn_decode_combine(part_o, part_ml, pos, qg, ldp, out, ldo, n, Hq, max_len, NS,

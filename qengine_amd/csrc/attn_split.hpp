@@ -7,6 +7,8 @@
 namespace qe {
 
 constexpr int TILE = 32;  // cache positions per wave step (two 16-row MFMA tiles)
+// rows of one decode call: the combine's grid has one y index per row (at most 65535)
+constexpr int MAX_DECODE_ROWS = 65535;
 
 // Division by NS as a multiply and a shift, computed once on the host (Granlund & Montgomery,
 // "Division by invariant integers using multiplication", 1994, Thm 4.2): with l = ceil(log2 NS)

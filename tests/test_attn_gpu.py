@@ -238,6 +238,43 @@ def test_gqa_shapes_and_rows(native, hq, hkv, n):
         assert torch.equal(o1[0], out[t]), t
 
 
+@pytest.mark.parametrize("hq,hkv,n,ns", [
+    (24, 4, 12, 16),    # GQA 6: row chunks of 8 + 4
+    (24, 4, 21, 52),    # 8 + 8 + 5 rows, the default split count of a 4-KV-head cache
+    (8, 1, 9, 8),       # GQA 8: chunks of 8 + 1
+    (32, 2, 6, 16),     # GQA 16: chunks of 4 + 2
+    (96, 1, 2, 16),     # GQA 96: one row and 48 + 48 q heads per launch
+    (130, 2, 2, 8),     # GQA 65: 32 + 33 q heads of each KV head per launch
+    (66, 1, 1, 4),
+])
+def test_wide_calls_run_as_several_launches(native, hq, hkv, n, ns):
+    """More than 8 rows or more than 64 query columns (group size x rows), which the reference
+    accepts (its rows are bounded only by part_o, any group size: csrc/bindings.cpp:176-179): the
+    partials run as several launches. Results match the oracle and each row is bit-identical to
+    a 1-row call."""
+    case = decode_case(seed=hq * 7 + n, hq=hq, hkv=hkv, pos=600, n=n, max_len=640)
+    out = gpu_decode(native, case, ns)
+    ok, mx, mean = attn_close(out, oracle_decode(case))
+    assert ok, (mx, mean)
+    for t in range(n):
+        o1 = gpu_decode(native, case, ns, pos=case.pos + t, rows=slice(t, t + 1))
+        assert torch.equal(o1[0], out[t]), t
+
+
+def test_wide_group_equals_its_sub_groups(native):
+    """A 96-head group (one KV head) runs as two launches of 48 q heads: each half of the output
+    equals, bit for bit, a 48-head call on the same cache with that half's q and gate rows."""
+    case = decode_case(seed=96, hq=96, hkv=1, pos=1500, n=2, max_len=1600)
+    out = gpu_decode(native, case, 16)
+    for h0 in (0, 48):
+        sub = copy.copy(case)
+        sub.q = case.q[:, h0 * D:(h0 + 48) * D].contiguous()
+        sub.qg = case.qg[:, h0 * 2 * D:(h0 + 48) * 2 * D].contiguous()
+        sub.hq = 48
+        half = gpu_decode(native, sub, 16)
+        assert torch.equal(half, out[:, h0 * D:(h0 + 48) * D]), h0
+
+
 @pytest.mark.parametrize("hq,hkv,n,pos,ns", [
     (24, 4, 2, 2047, 64),   # lengths 2048 | 2049: slices of 32 | 64 (one column tile)
     (24, 4, 5, 2046, 64),   # 2 + 3 rows (two column tiles)

@@ -75,9 +75,8 @@ A = 1 << 20
 
 
 @pytest.mark.parametrize("kw,why", [
-    (dict(n=0), "no rows"), (dict(n=9), "more than 8 rows"), (dict(hq=25), "Hq % Hkv"),
-    (dict(hq=68, hkv=1, n=1), "group*n > 64"), (dict(hq=24, n=3, hkv=1), "group*n > 64"),
-    (dict(ns=0), "no splits"), (dict(max_len=0), "empty cache"),
+    (dict(n=0), "no rows"), (dict(n=65536), "more rows than the combine's grid"),
+    (dict(hq=25), "Hq % Hkv"), (dict(ns=0), "no splits"), (dict(max_len=0), "empty cache"),
     (dict(max_len=1 << 23), "cache beyond 32-bit buffer offsets"),
     (dict(q=A + 8), "unaligned q"), (dict(kc=A + 2), "unaligned kc"),
 ])
@@ -173,8 +172,9 @@ def test_capi_prep_rejects(capi, kw, why):
 
 
 @pytest.mark.parametrize("kw,why", [
-    (dict(n=0), "no rows"), (dict(n=9), "more than 8 rows"), (dict(rd=3), "odd rotary dims"),
-    (dict(hq=25), "Hq % Hkv"), (dict(ns=0), "no splits"), (dict(q_out=A + 8), "unaligned q_out"),
+    (dict(n=0), "no rows"), (dict(n=65536), "more than 65535 rows"),
+    (dict(rd=3), "odd rotary dims"), (dict(hq=25), "Hq % Hkv"), (dict(ns=0), "no splits"),
+    (dict(q_out=A + 8), "unaligned q_out"),
     (dict(qg=None), "null qg"), (dict(out=None), "null out"),
     (dict(max_len=1 << 23), "cache beyond 32-bit buffer offsets"),
 ])
@@ -256,10 +256,23 @@ def test_decode_contract_rejects(native, mutate, msg):
 
 
 def test_decode_contract_row_limits(native):
-    with pytest.raises(RuntimeError, match="1..8 rows"):
-        check_decode(native, decode_args(n=9))
-    with pytest.raises(RuntimeError, match="<= 64"):
-        check_decode(native, decode_args(n=8, hq=32, hkv=2))   # 16 * 8 = 128 columns
+    """Rows are bounded only by part_o.size(0) (and the combine's 65535), any group size is
+    accepted, as in the reference (csrc/bindings.cpp:176-179): wider calls run as several
+    partials launches."""
+    assert check_decode(native, decode_args(n=9))[0] == 9
+    assert check_decode(native, decode_args(n=8, hq=32, hkv=2))[:3] == [8, 32, 2]  # 128 columns
+    assert check_decode(native, decode_args(n=1, hq=130, hkv=1))[:3] == [1, 130, 1]
+    with pytest.raises(RuntimeError, match="1..65535 rows"):
+        a = decode_args(n=1, hq=1, hkv=1)
+        a["q"], a["out"] = torch.empty(65536, D, dtype=BF), torch.empty(65536, D, dtype=BF)
+        a["qg"] = torch.empty(65536, 2 * D, dtype=BF)
+        a["part_o"] = torch.empty(65536, 1, 4, D, dtype=F32)
+        a["part_ml"] = torch.empty(65536, 1, 4, 2, dtype=F32)
+        check_decode(native, a)
+    with pytest.raises(RuntimeError, match="part_o"):
+        a = decode_args(n=9)
+        a["part_o"], a["part_ml"] = a["part_o"][:8], a["part_ml"][:8]
+        check_decode(native, a)
 
 
 def test_decode_requires_gpu_tensors(native):

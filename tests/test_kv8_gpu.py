@@ -65,6 +65,19 @@ def test_fp8_scale_one_equals_bf16_on_the_dequantized_cache(native, hq, hkv, n, 
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
+@pytest.mark.parametrize("hq,hkv,n,ns", [(24, 4, 13, 64), (96, 1, 2, 16), (130, 2, 1, 8)])
+def test_fp8_wide_calls_equal_bf16(native, hq, hkv, n, ns):
+    """More than 8 rows or more than 64 q heads per KV head over the fp8 cache (several partials
+    launches): scale-1 output equals the bf16 path on the dequantized cache bit for bit."""
+    case = decode_case(seed=hq + n, hq=hq, hkv=hkv, pos=900, n=n, max_len=1000)
+    kc8, vc8 = quantize_cache(case.kc, 1.0), quantize_cache(case.vc, 1.0)
+    kd = K8.dequantize(kc8.view(torch.uint8), 1.0).to(BF)
+    vd = K8.dequantize(vc8.view(torch.uint8), 1.0).to(BF)
+    a = run_fp8(native, case.q, case.qg, kc8, vc8, case.pos, ns, 1.0, 1.0)
+    b = run_bf16(native, case.q, case.qg, kd, vd, case.pos, ns)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
 @pytest.mark.parametrize("ks,vs", [(1.0, 1.0), (0.5, 0.25), (0.037, 0.011), (3.0, 2.0)])
 @pytest.mark.parametrize("n,pos,max_len", [(1, 4095, 4096), (5, 4096, 4101), (2, 300, 20000)])
 def test_fp8_decode_vs_oracle(native, ks, vs, n, pos, max_len):

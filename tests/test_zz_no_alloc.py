@@ -87,6 +87,8 @@ def test_noalloc_rejects_oversized_calls(capi):
     ns_over = cap // (8 * 24) + 1
     assert capi.decode_noalloc(q, kc, vc, p, qg, 48 * D, out, 24 * D, 8, 24, 4, 256,
                                ns_over) == INVALID
-    assert capi.decode_noalloc(q, kc, vc, p, qg, 48 * D, out, 24 * D, 9, 24, 4, 256,
+    assert capi.decode_noalloc(q, kc, vc, p, qg, 48 * D, out, 24 * D, 65536, 24, 4, 256,
+                               4) == INVALID
+    assert capi.decode_noalloc(q, kc, vc, p, qg, 48 * D, out, 24 * D, 8, 25, 4, 256,
                                4) == INVALID
     torch.cuda.synchronize()
