@@ -133,14 +133,22 @@ __device__ __forceinline__ void issue_tile8(u32x4_t* stage, __amdgpu_buffer_rsrc
 }
 
 // Thread i of the workgroup converts the 16 codes of fp8 chunk i (row i/16, dims 16(i%16) ..) of
-// the K and the V tile into two bf16 chunks each, at their swizzled bf16 slots.
+// the K and the V tile into two bf16 chunks each, at their swizzled bf16 slots. The 16 threads of
+// a row write bf16 chunks 2c + p then 2c + 1 - p (c = i % 16, p = bit 2 ^ bit 3 of c), so each
+// store's 8 (and 16) consecutive lanes hit distinct 16-byte bank groups: with p = 0 for all, the
+// even chunks of the first store fall on half the groups (2-way conflicts). The row swizzles
+// XOR a chunk index with a per-row constant, which keeps the groups distinct.
 __device__ __forceinline__ void convert_tile8(const u32x4_t* stage, u32x4_t* bf) {
-  const int i = threadIdx.x, r = i >> 4, q = (i & 15) * 2;
+  const int i = threadIdx.x, r = i >> 4, c = i & 15, q = 2 * c;
+  const int p = ((c >> 2) ^ (c >> 3)) & 1;
   const u32x4_t kk = stage[i], vv = stage[TILE8_U4 + i];
-  bf[tile::k_slot(r, q)] = fp8x8_to_bf16x8(u32x2_t{kk[0], kk[1]});
-  bf[tile::k_slot(r, q + 1)] = fp8x8_to_bf16x8(u32x2_t{kk[2], kk[3]});
-  bf[TILE_U4 + r * ROW_CHUNKS + (q ^ tile::v_swz(r))] = fp8x8_to_bf16x8(u32x2_t{vv[0], vv[1]});
-  bf[TILE_U4 + r * ROW_CHUNKS + ((q + 1) ^ tile::v_swz(r))] = fp8x8_to_bf16x8(u32x2_t{vv[2], vv[3]});
+  // the codes of chunk q + p (first store) and q + 1 - p (second), selected before conversion
+  const u32x2_t ka{p ? kk[2] : kk[0], p ? kk[3] : kk[1]}, kb{p ? kk[0] : kk[2], p ? kk[1] : kk[3]};
+  const u32x2_t va{p ? vv[2] : vv[0], p ? vv[3] : vv[1]}, vb{p ? vv[0] : vv[2], p ? vv[1] : vv[3]};
+  bf[tile::k_slot(r, q + p)] = fp8x8_to_bf16x8(ka);
+  bf[tile::k_slot(r, q + 1 - p)] = fp8x8_to_bf16x8(kb);
+  bf[TILE_U4 + r * ROW_CHUNKS + ((q + p) ^ tile::v_swz(r))] = fp8x8_to_bf16x8(va);
+  bf[TILE_U4 + r * ROW_CHUNKS + ((q + 1 - p) ^ tile::v_swz(r))] = fp8x8_to_bf16x8(vb);
 }
 
 // run_tiles for the fp8 cache: iteration j converts tile j into bf16 pair j % 2 (whose previous
