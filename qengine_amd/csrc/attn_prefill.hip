@@ -62,6 +62,11 @@ constexpr int LOADS_PER_TILE = 2 * LOAD_INSTR;   // K then V
 static_assert(LOAD_ROWS % 2 == 0 && LOADS_PER_TILE * AHEAD < 64, "tile split over the waves");
 constexpr int PF_CPOL = 0;                      // cached loads: every row block re-reads its KV head
 constexpr int XCDS = 8;                         // MI355X: 8 XCDs, each with its own L2
+// Operand reads kept ahead of the MFMAs in a tile's S^T and O^T steps (tile::qk_tile / pv_tile_tr
+// LEAD: 4 K reads, the V^T reads of 4 M-tiles). Max-ILP alone measured 172.2 us at config 5
+// (balanced kernel, bf16 cache, one-process A/B); leads 2 / 4 / 6 / 8 gave 171.0 / 169.4 /
+// 168.4 / 183.8 (bits identical).
+constexpr int SG_LEAD = 4;
 
 // Issue this wave's LDS-DMA loads of tile [p0, p0 + 32): rows LOAD_ROWS*w .. +LOAD_ROWS of K
 // and of V (both swizzled: lane i fetches the chunk that belongs in slot 64j + i).
@@ -105,11 +110,11 @@ __device__ __forceinline__ void run_tiles(int j0, int j1, int Lwave, u32x4_t* ld
       issue_tile(lds + ((j + AHEAD) % STAGES) * STAGE_U4, krs, vrs, p0 + AHEAD * BN, w, lane);
     if (p0 >= Lwave) continue;      // tiles past this wave's rows contribute nothing
     f32x4_t sacc[NT][2];
-    tile::qk_tile<NT, NT == 1>(kt, qb, c, g4, sacc);
+    tile::qk_tile<NT, NT == 1, SG_LEAD>(kt, qb, c, g4, sacc);
     u32x4_t pb_hi[NT], pb_lo[NT];
     tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc, pb_hi,
                                         pb_lo);
-    tile::pv_tile_tr<NT, SPLIT, NT == 1>(vt, lane, g4, pb_hi, pb_lo, st.acc);
+    tile::pv_tile_tr<NT, SPLIT, NT == 1, SG_LEAD>(vt, lane, g4, pb_hi, pb_lo, st.acc);
   }
 }
 
@@ -170,11 +175,11 @@ __device__ __forceinline__ void run_tiles8(int j0, int j1, int Lwave, u32x4_t* l
     lds_barrier();  // the bf16 tile is complete
     if (p0 >= Lwave) continue;
     f32x4_t sacc[NT][2];
-    tile::qk_tile<NT, NT == 1>(bf, qb, c, g4, sacc);
+    tile::qk_tile<NT, NT == 1, SG_LEAD>(bf, qb, c, g4, sacc);
     u32x4_t pb_hi[NT], pb_lo[NT];
     tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc, pb_hi,
                                         pb_lo);
-    tile::pv_tile_tr<NT, SPLIT, NT == 1>(bf + TILE_U4, lane, g4, pb_hi, pb_lo, st.acc);
+    tile::pv_tile_tr<NT, SPLIT, NT == 1, SG_LEAD>(bf + TILE_U4, lane, g4, pb_hi, pb_lo, st.acc);
   }
 }
 
@@ -338,11 +343,11 @@ __device__ __forceinline__ void run_tiles_bal(int j0, int j1, int Lwave, u32x4_t
                  lane);
     if (p0 >= Lwave) continue;
     f32x4_t sacc[NT][2];
-    tile::qk_tile<NT, NT == 1>(kt, qb, c, g4, sacc);
+    tile::qk_tile<NT, NT == 1, SG_LEAD>(kt, qb, c, g4, sacc);
     u32x4_t pb_hi[NT], pb_lo[NT];
     tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc, pb_hi,
                                         pb_lo);
-    tile::pv_tile_tr<NT, SPLIT, NT == 1>(vt, lane, g4, pb_hi, pb_lo, st.acc);
+    tile::pv_tile_tr<NT, SPLIT, NT == 1, SG_LEAD>(vt, lane, g4, pb_hi, pb_lo, st.acc);
   }
 }
 
@@ -369,11 +374,11 @@ __device__ __forceinline__ void run_tiles_bal8(int j0, int j1, int Lwave, u32x4_
     if (p0 >= Lwave) continue;
     const u32x4_t* bf = bfp + (j & 1) * STAGE_U4;
     f32x4_t sacc[NT][2];
-    tile::qk_tile<NT, NT == 1>(bf, qb, c, g4, sacc);
+    tile::qk_tile<NT, NT == 1, SG_LEAD>(bf, qb, c, g4, sacc);
     u32x4_t pb_hi[NT], pb_lo[NT];
     tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc, pb_hi,
                                         pb_lo);
-    tile::pv_tile_tr<NT, SPLIT, NT == 1>(bf + TILE_U4, lane, g4, pb_hi, pb_lo, st.acc);
+    tile::pv_tile_tr<NT, SPLIT, NT == 1, SG_LEAD>(bf + TILE_U4, lane, g4, pb_hi, pb_lo, st.acc);
   }
 }
 
