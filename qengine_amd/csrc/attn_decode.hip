@@ -935,6 +935,12 @@ constexpr int REGION_U4 = 2 * TILE_U4;       // a subset's K tile then V tile
 // it waits for it before the first read).
 namespace cols {
 constexpr int STAGE8_U4 = TILE * HD / 16;  // 16-byte slots of one fp8 tile: 8 KB
+// Operand reads kept ahead of the MFMAs in S^T and O^T (tile::qk_tile / pv_tile_tr LEAD) at one
+// column tile per wave. Same-box harness A/B, partials us, none -> 4: 5 rows at 4101 (config 3)
+// 10.64 -> 10.42, 8 rows at 4104 13.45 -> 13.39, 8 rows at 16392 22.80 -> 22.49; bits identical.
+// Two column tiles per wave already spill and keep the compiler's order.
+template <int CPW>
+constexpr int LEAD = CPW == 1 ? 4 : 0;
 
 // 16 one-KB LDS-DMA loads of a bf16 K (or V) tile, rows 2i, 2i+1, shared by the subset's waves
 template <bool IS_V>
@@ -972,7 +978,7 @@ __device__ __forceinline__ void qk_softmax_half(
   if (load) issue<LD>(rs, p_load, dst, rank, wps, lane);
   if (!has) return;
   f32x4_t sacc[CPW][2];
-  tile::qk_tile<CPW>(kt, qb, c, g4, sacc);
+  tile::qk_tile<CPW, false, LEAD<CPW>>(kt, qb, c, g4, sacc);
   if (p0 + TILE > Lmin)
     tile::softmax_tile<CPW, true, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
   else
@@ -986,7 +992,7 @@ __device__ __forceinline__ void pv_half_la(const u32x4_t* __restrict__ vt,
                                            const u32x4_t (&pb_hi)[CPW], const u32x4_t (&pb_lo)[CPW],
                                            f32x4_t (&acc)[CPW][16]) {
   if (load) issue<LD>(rs, p_load, dst, rank, wps, lane);
-  if (has) tile::pv_tile_tr<CPW, true>(vt, lane, g4, pb_hi, pb_lo, acc);
+  if (has) tile::pv_tile_tr<CPW, true, false, LEAD<CPW>>(vt, lane, g4, pb_hi, pb_lo, acc);
 }
 // All NTH threads of the workgroup convert the fp8 tiles of the first nact subsets once, from
 // `src` (row-major) to `dst` (the bf16 K or V tile layout) in each subset's region of `region`
@@ -1256,14 +1262,14 @@ attn_partials_cols_kernel(const __bf16* __restrict__ q, const __bf16* __restrict
       f32x4_t sacc[CPW][2];
       u32x4_t pb_hi[CPW], pb_lo[CPW];
       if (has) {
-        tile::qk_tile<CPW>(kt, qb, c, g4, sacc);
+        tile::qk_tile<CPW, false, cols::LEAD<CPW>>(kt, qb, c, g4, sacc);
         if (p0 + TILE > P.Lmin)
           tile::softmax_tile<CPW, true, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
         else
           tile::softmax_tile<CPW, false, true>(sacc, p0, Lcol, scale_log2, g4, m, l, acc, pb_hi, pb_lo);
       }
       if constexpr (KV8) __syncthreads();  // the bf16 V tile is whole
-      if (has) tile::pv_tile_tr<CPW, true>(vt, lane, g4, pb_hi, pb_lo, acc);
+      if (has) tile::pv_tile_tr<CPW, true, false, cols::LEAD<CPW>>(vt, lane, g4, pb_hi, pb_lo, acc);
       __syncthreads();  // this round's tiles are read before the next round overwrites them
     }
 

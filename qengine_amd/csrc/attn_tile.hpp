@@ -36,9 +36,9 @@ __device__ __forceinline__ int k_slot(int r, int q) { return r * ROW_CHUNKS + (q
 // XA (NT == 1; the K tile 256-byte aligned in LDS): the four bases are one per-lane base XORed
 // with 64 (ks & 3), since 64 (l ^ (c >> 2)) = 64 l ^ 64 (c >> 2) touches address bits 6-7 only:
 // the same addresses, formed per tile instead of living across the caller's loop.
-// LEAD > 0 (NT == 1 with XA): the tile's 16 K operand reads and 16 MFMAs are scheduled as LEAD
-// reads, then (1 MFMA, 1 read) pairs, then the last LEAD MFMAs (sched_group_barrier), so LEAD
-// reads stay in flight ahead of the MFMA that needs them.
+// LEAD > 0: the tile's 16 K operand reads and 16 NT MFMAs are scheduled as LEAD reads, then
+// (NT MFMAs, 1 read) groups, then the last LEAD NT MFMAs (sched_group_barrier), so LEAD reads
+// stay in flight ahead of the MFMAs that need them.
 template <int NT, bool XA = false, int LEAD = 0>
 __device__ __forceinline__ void qk_tile(const u32x4_t* k_lds, const bf16x8_t (&qb)[NT][8], int c,
                                         int g4, f32x4_t (&sacc)[NT][2]) {
@@ -65,14 +65,14 @@ __device__ __forceinline__ void qk_tile(const u32x4_t* k_lds, const bf16x8_t (&q
       for (int ct = 0; ct < NT; ++ct) sacc[ct][T] = mfma16x16x32(kop, qb[ct][ks], sacc[ct][T]);
     }
   }
-  if constexpr (LEAD > 0 && XA && NT == 1) {
-    __builtin_amdgcn_sched_group_barrier(0x100, LEAD, 0);  // LDS reads
+  if constexpr (LEAD > 0) {
+    __builtin_amdgcn_sched_group_barrier(0x100, LEAD, 0);   // LDS reads
 #pragma unroll
     for (int i = 0; i < 16 - LEAD; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x008, NT, 0);   // MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, LEAD, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, LEAD * NT, 0);
   }
 }
 
@@ -173,8 +173,9 @@ __device__ __forceinline__ int v_swz(int r) { return 2 * (r & 7); }
 // XA (NT == 1; the V tile 256-byte aligned in LDS): the eight bases are one per-lane base XORed
 // with 32 (i & 7) (32 (l ^ (r & 7)) = 32 l ^ 32 (r & 7) touches address bits 5-7 only), formed
 // per tile instead of living across the caller's loop: 13 fewer registers in the prefill kernel.
-// LEAD > 0 (NT == 1 with XA, one P term): the 32 transposing reads and 16 MFMAs are scheduled as
-// the reads of LEAD M-tiles, then (1 MFMA, 2 reads) groups, then the last LEAD MFMAs.
+// LEAD > 0: the 32 transposing reads and the MFMAs of the 16 M-tiles (NT, or 2 NT with SPLIT,
+// each) are scheduled as the reads of LEAD M-tiles, then (one M-tile's MFMAs, 2 reads) groups,
+// then the last LEAD M-tiles' MFMAs.
 template <int NT, bool SPLIT, bool XA = false, int LEAD = 0>
 __device__ __forceinline__ void pv_tile_tr(const u32x4_t* vt, int lane, int g4,
                                            const u32x4_t (&pb_hi)[NT], const u32x4_t (&pb_lo)[NT],
@@ -211,14 +212,15 @@ __device__ __forceinline__ void pv_tile_tr(const u32x4_t* vt, int lane, int g4,
         acc[ct][i] = mfma16x16x32(as_bf16x8(av), as_bf16x8(pb_lo[ct]), acc[ct][i]);
     }
   }
-  if constexpr (LEAD > 0 && XA && NT == 1 && !SPLIT) {
+  if constexpr (LEAD > 0) {
+    constexpr int MPT = NT * (SPLIT ? 2 : 1);  // MFMAs per M-tile
     __builtin_amdgcn_sched_group_barrier(0x100, 2 * LEAD, 0);  // LDS reads
 #pragma unroll
     for (int i = 0; i < 16 - LEAD; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x008, MPT, 0);     // MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, LEAD, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, LEAD * MPT, 0);
   }
 }
 
