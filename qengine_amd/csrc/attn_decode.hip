@@ -178,7 +178,11 @@ __device__ __forceinline__ void compute_tile(const VTile& b, const u32x4_t* ks_l
                                              f32x4_t (&acc)[NT][16]) {
   wave_lds_fence();
   f32x4_t sacc[NT][2];
-  tile::qk_tile<NT, NT == 1>(ks_lds, qb, c, g4, sacc);  // (K tiles 256-byte aligned)
+  // (K tiles 256-byte aligned.) Two column tiles: the K reads are scheduled two ahead of their
+  // MFMA pairs (tile::qk_tile LEAD). Same-box harness A/B, partials us, none -> 2: 3 rows at
+  // 16387 17.73 -> 17.45, 5 rows at 16389 18.28 -> 18.01, 4 rows at 8196 13.41 -> 13.25, 5 rows
+  // at 32773 27.64 -> 27.44 (leads 4 and 6: no gain); bits identical. One tile: no change.
+  tile::qk_tile<NT, NT == 1, NT == 2 ? 2 : 0>(ks_lds, qb, c, g4, sacc);
   wave_lds_fence();  // this tile's K reads happen before the next tile's LDS-DMA writes
   u32x4_t pb_hi[NT], pb_lo[NT];
   if (p0 + TILE > Lmin)
