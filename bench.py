@@ -168,6 +168,10 @@ MIN_WARMUP_SECONDS = 0.1  # and at least this long per graph: clocks ramp over t
 # MFMA-bound graphs (the prefill legs) take longer to reach steady clocks: after 0.1 s of replays
 # the first timing of a prefill graph read 5-10% slow in same-process A/Bs on MI355X
 MIN_WARMUP_SECONDS_MFMA = 1.0
+# prefill calls per graph: a model's prefill runs its attention layers back to back in one graph,
+# as the decode legs time 16 layer-calls per graph; one call per graph adds the graph launch to
+# every call (reported as *_1call)
+PREFILL_CALLS = 8
 
 
 class Timing:
@@ -665,7 +669,8 @@ def bench_gdn(torch, C, steps: int, warmup: int, rows=(1, 2, 4, 6, 8)) -> dict:
 
 def bench_prefill(torch, C, steps: int, warmup: int) -> dict:
     """a 2048-row causal chunk appended to a 2048-position cache (attn_prep_chunk
-    + attn_prefill), timed as graph replays. FLOPs = 4 * D * Hq * sum of attended lengths."""
+    + attn_prefill), timed as replays of graphs holding PREFILL_CALLS calls (values per call), and
+    of graphs holding one call (``*_1call``). FLOPs = 4 * D * Hq * sum of attended lengths."""
     dev, BF = "cuda", torch.bfloat16
     gen = torch.Generator(device=dev).manual_seed(5)
     res = {}
@@ -686,16 +691,23 @@ def bench_prefill(torch, C, steps: int, warmup: int) -> dict:
     C.attn_prep_chunk(qgT, kT, vT, qnw, knw, inv, posT, qT, kc, vc, 1e-6)
     flops = 4 * D * HQ * sum(pos0 + 1 + t for t in range(T))
     mw = MIN_WARMUP_SECONDS_MFMA
-    ms_attn = time_fn_graph(torch, lambda: C.attn_prefill(qT, kc, vc, posT, qgT, outT), steps, warmup,
-                            mw)
+    nc = PREFILL_CALLS
+
+    def per_call(fn):  # ms per call: graphs of nc calls, and graphs of one
+        many = time_fn_graph(torch, lambda: [fn() for _ in range(nc)], steps, warmup, mw) / nc
+        return many, time_fn_graph(torch, fn, steps, warmup, mw)
+
+    ms_attn, ms_attn1 = per_call(lambda: C.attn_prefill(qT, kc, vc, posT, qgT, outT))
 
     def full():
         C.attn_prep_chunk(qgT, kT, vT, qnw, knw, inv, posT, qT, kc, vc, 1e-6)
         C.attn_prefill(qT, kc, vc, posT, qgT, outT)
-    ms_full = time_fn_graph(torch, full, steps, warmup, mw)
+    ms_full, ms_full1 = per_call(full)
     tflops = flops / (ms_attn * 1e-3) / 1e12
     res["cfg5_prefill_2048_on_2048"] = {
         "us_attention": round(ms_attn * 1e3, 2), "us_prep_plus_attention": round(ms_full * 1e3, 2),
+        "calls_per_graph": nc, "us_attention_1call": round(ms_attn1 * 1e3, 2),
+        "us_prep_plus_attention_1call": round(ms_full1 * 1e3, 2),
         "GFLOP": round(flops / 1e9, 2), "TFLOPs": round(tflops, 1),
         "mfma_frac_of_2500_TFLOPs_bf16_dense": round(tflops / 2500.0, 4)}
 
@@ -707,16 +719,17 @@ def bench_prefill(torch, C, steps: int, warmup: int) -> dict:
     kc8.copy_((kc.float() * 16).clamp(-448, 448).to(torch.float8_e4m3fn))
     vc8.copy_((vc.float() * 16).clamp(-448, 448).to(torch.float8_e4m3fn))
     C.attn_prep_fp8(qgT, kT, vT, qnw, knw, inv, posT, qT, kc8, vc8, 1e-6, ks, vs)
-    ms8 = time_fn_graph(torch, lambda: C.attn_prefill_fp8(qT, kc8, vc8, posT, qgT, outT, ks, vs),
-                        steps, warmup, mw)
+    ms8, ms8_1 = per_call(lambda: C.attn_prefill_fp8(qT, kc8, vc8, posT, qgT, outT, ks, vs))
 
     def full8():
         C.attn_prep_fp8(qgT, kT, vT, qnw, knw, inv, posT, qT, kc8, vc8, 1e-6, ks, vs)
         C.attn_prefill_fp8(qT, kc8, vc8, posT, qgT, outT, ks, vs)
-    ms8_full = time_fn_graph(torch, full8, steps, warmup, mw)
+    ms8_full, ms8_full1 = per_call(full8)
     tf8 = flops / (ms8 * 1e-3) / 1e12
     res["cfg5_prefill_fp8kv"] = {
         "us_attention": round(ms8 * 1e3, 2), "us_prep_plus_attention": round(ms8_full * 1e3, 2),
+        "calls_per_graph": nc, "us_attention_1call": round(ms8_1 * 1e3, 2),
+        "us_prep_plus_attention_1call": round(ms8_full1 * 1e3, 2),
         "TFLOPs": round(tf8, 1), "mfma_frac_of_2500_TFLOPs_bf16_dense": round(tf8 / 2500.0, 4)}
     return res
 
