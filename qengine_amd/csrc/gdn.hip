@@ -19,7 +19,8 @@
 // gfx950 layout: one workgroup of NT = 1024 threads (16 waves, four per SIMD) per value head.
 // With NC = 2048 / NT state columns per lane, wave w owns columns 4 NC w .. +4 NC - 1 and lane l
 // holds rows 8(l>>2) .. +7 of columns 4 NC w + NC (l&3) .. +NC - 1 (16 fp32 registers at NC = 2,
-// loaded as eight 8-byte rows; NT = 512 gives NC = 4, 32 registers). Per delta-rule step the CU
+// loaded as eight 8-byte rows, or for 1-2 rows through a 64 KB LDS copy read and written as whole
+// rows; NT = 512 gives NC = 4, 32 registers). Per delta-rule step the CU
 // runs the same 3 x 16,384 fp32 operations either way; 16 waves hide more of the butterflies'
 // and LDS latencies than 8 (same-box A/B on MI355X at Hk 16 / Hv 48, us per call at 1 / 2 / 3 /
 // 4 rows: 8.60 / 10.16 / 11.57 / 12.35 with 8 waves (the split path at 4) against 8.44 / 9.50 /
@@ -42,7 +43,7 @@
 
 namespace qe {
 
-template <int NT>
+template <int NT, bool SL>
 __global__ void __launch_bounds__(NT)
 gdn_step_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
                 const __bf16* __restrict__ b, const __bf16* __restrict__ a, long ldp,
@@ -56,8 +57,16 @@ gdn_step_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
   __shared__ __align__(16) float qa[GDN_MAXN][GDN_D], ka[GDN_MAXN][GDN_D], va[GDN_MAXN][GDN_D];
   __shared__ __align__(16) float oa[GDN_MAXN][GDN_D];
   __shared__ float sg[GDN_MAXN][2], ga[GDN_MAXN][2], l2p[GDN_MAXN][4];
+  // SL: the state is staged through LDS. It is read and written back as whole 512-byte rows
+  // (coalesced, four 16-byte pieces per thread) and moved to and from the register layout in
+  // LDS. Float (r, c) sits at r*128 + 8((c/8) ^ (r/8 & 15)) + c%8, so the 16 rows of one
+  // register-layout access (stride 8 rows) hit distinct 32-byte groups. Direct loads in the
+  // register layout read 32 bytes of each 128-byte line per wave.
+  __shared__ __align__(16) float sS[SL ? GDN_D * GDN_D : 4];
+  auto sidx = [](int r, int c) { return r * GDN_D + 8 * ((c >> 3) ^ ((r >> 3) & 15)) + (c & 7); };
 
   static_assert(NT == 512 || NT == 1024, "8 or 16 waves");
+  static_assert(!SL || NT == 1024, "the staged state: four 16-byte pieces per thread");
   constexpr int NC = 2048 / NT;  // state columns per lane: 4 (8 waves) or 2 (16 waves)
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int rg = lane >> 2, col0 = 4 * NC * w + NC * (lane & 3);
@@ -97,7 +106,13 @@ gdn_step_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
               : st_v + ((size_t)srow * Hv + j) * GDN_D + 4 * (su - 32));
   const float2 stg = *reinterpret_cast<const float2*>(st_g + ((size_t)(tid & 7) * Hv + j) * 2);
   float s[8][NC];
-  load_state_rows(Sj, rg, col0, s);
+  F4 gS[SL ? 4 : 1];  // SL: pieces f = tid + NT k, row f / 32, columns 4 (f % 32) .. +3
+  if constexpr (SL) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) gS[k] = reinterpret_cast<const F4*>(Sj)[tid + NT * k];
+  } else {
+    load_state_rows(Sj, rg, col0, s);
+  }
 
   if (tid < GDN_MAXN * 64)
     *reinterpret_cast<F4*>(su < 32 ? &sk[srow][4 * su] : &sv[srow][4 * (su - 32)]) = stv;
@@ -137,7 +152,22 @@ gdn_step_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
     ga[gt][0] = gv.x;
     ga[gt][1] = gv.y;
   }
+  if constexpr (SL) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int f = tid + NT * k;
+      *reinterpret_cast<F4*>(&sS[sidx(f >> 5, 4 * (f & 31))]) = gS[k];
+    }
+  }
   __syncthreads();
+  if constexpr (SL) {  // each lane reads (and later writes) only its own elements
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+      const float2 v = *reinterpret_cast<const float2*>(&sS[sidx(rg * 8 + rr, col0)]);
+      s[rr][0] = v.x;
+      s[rr][NC - 1] = v.y;
+    }
+  }
 
   // Stage this call's v and gates for the next call's replay. Only after the barrier: the staged
   // rows of the previous call (same addresses) have all been read into LDS by then.
@@ -171,8 +201,24 @@ gdn_step_kernel(const __bf16* __restrict__ qkv, const __bf16* __restrict__ z,
     vec_read_n(&sv[t][col0], v);
     delta_step(s, k, v, sg[t][0], sg[t][1]);
   }
-  if (pend > 0) store_state_rows(Sj, rg, col0, s);
-  __syncthreads();
+  if constexpr (SL) {
+    if (pend > 0) {
+#pragma unroll
+      for (int rr = 0; rr < 8; ++rr)
+        *reinterpret_cast<float2*>(&sS[sidx(rg * 8 + rr, col0)]) = make_float2(s[rr][0], s[rr][NC - 1]);
+    }
+    __syncthreads();
+    if (pend > 0) {  // the copy runs beside the new rows, which do not touch sS
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int f = tid + NT * k;
+        reinterpret_cast<F4*>(Sj)[f] = *reinterpret_cast<const F4*>(&sS[sidx(f >> 5, 4 * (f & 31))]);
+      }
+    }
+  } else {
+    if (pend > 0) store_state_rows(Sj, rg, col0, s);
+    __syncthreads();
+  }
 
   // ---- 2. new rows on the register copy ----
   for (int t = 0; t < n; ++t) {
@@ -222,7 +268,11 @@ extern "C" hipError_t qe_gdn_step_n(const void* qkv, const void* z, const void* 
                             static_cast<const __bf16*>(A_log), static_cast<const __bf16*>(dt_bias),
                             static_cast<const __bf16*>(norm_w), S, st_k, st_v, st_g, ctl,
                             static_cast<__bf16*>(out), ldo, n, Hk, Hv, eps, stream);
-  gdn_step_kernel<GDN_THREADS><<<dim3(Hv), dim3(GDN_THREADS), 0, stream>>>(
+  // 1-2 rows stage the state through LDS (same bits; same-box A/B, us per call at 1 / 2 / 3 / 4
+  // rows: 8.41 / 9.44 / 10.65 / 12.01 direct, 7.73 / 9.21 / 10.66 / 12.10 staged)
+  auto kern = n <= GDN_STAGE_MAX_ROWS ? gdn_step_kernel<GDN_THREADS, true>
+                                      : gdn_step_kernel<GDN_THREADS, false>;
+  kern<<<dim3(Hv), dim3(GDN_THREADS), 0, stream>>>(
       static_cast<const __bf16*>(qkv), static_cast<const __bf16*>(z), static_cast<const __bf16*>(b),
       static_cast<const __bf16*>(a), ldp, static_cast<__bf16*>(ring),
       static_cast<const __bf16*>(conv_w), static_cast<const __bf16*>(A_log),

@@ -18,6 +18,7 @@ constexpr int GDN_SPLIT = 4;                        // workgroups per head in th
 constexpr int GDN_SPLIT_COLS = GDN_D / GDN_SPLIT;
 constexpr int GDN_SPLIT_THREADS = 512;
 constexpr int GDN_SPLIT_MIN_ROWS = 5;               // fewer rows: the one-workgroup kernel
+constexpr int GDN_STAGE_MAX_ROWS = 2;               // up to this many: the state staged in LDS
 
 struct __align__(16) F4 {
   float x, y, z, w;
