@@ -90,6 +90,160 @@ attn_prep_kernel(const __bf16* __restrict__ qg, const __bf16* __restrict__ k,
   }
 }
 
+// One head per half-wave, eight heads of R consecutive rows per 256-thread workgroup: lane L of
+// the half-wave owns dims 8L .. 8L+7 of each row (16-byte loads and stores), and all R rows'
+// loads are issued before the first row is normalised.
+// The arithmetic is prep_dim's, to the bit: the sum of squares of each 64-dim group follows
+// wave_sum_fast's butterfly (dims c and c^32, c^16, c^8 sit in lanes L^4, L^2, L^1 at the same
+// slot; c^4, c^2, c^1 in slots k^4, k^2, k^1 of the same lane), and the four group sums are added
+// in the order ((r0 + r1) + r2) + r3. The rotary cos/sin of the rows' rd/2 frequencies (fp64
+// cos/sin, the kernel's most expensive step) are computed once per workgroup into an LDS table
+// (one workgroup barrier); the rotate_half partner goes through the half-wave's own LDS row.
+// Needs 16-byte aligned rows (checked by the launcher; otherwise attn_prep_kernel runs).
+// 2048-row chunk at 24 Q / 4 KV heads, same box: 33.4 us for attn_prep_kernel<false, 8>, about
+// 21 us here (the launcher's R).
+template <bool FP8, int R>
+__global__ void __launch_bounds__(HD)
+attn_prep_rows_kernel(const __bf16* __restrict__ qg, const __bf16* __restrict__ k,
+                      const __bf16* __restrict__ v, long ldp, const __bf16* __restrict__ qnw,
+                      const __bf16* __restrict__ knw, const float* __restrict__ inv_freq,
+                      const int* __restrict__ pos_ptr, __bf16* __restrict__ q_out,
+                      void* __restrict__ kc, void* __restrict__ vc, int n, int Hq, int Hkv,
+                      int max_len, int rd, float eps, float k_inv, float v_inv) {
+  constexpr int HW = 32;                   // lanes per head
+  constexpr int UPW = HD / HW;             // heads per workgroup
+  constexpr int TE = (R * (HD / 2) + HD - 1) / HD;  // table entries per thread, at most
+  __shared__ float xn_all[UPW][HD];        // per half-wave: the normalised row
+  __shared__ float2 cst[R][HD / 2];        // cos/sin of the rows' rd/2 frequencies
+  const int tid = threadIdx.x, hw = tid / HW, L = tid & (HW - 1);
+  const int nh = Hq + Hkv, wpr = (nh + UPW - 1) / UPW;  // workgroups per row group
+  const int grp = blockIdx.x / wpr, t0 = grp * R;
+  const int hb_raw = (blockIdx.x - grp * wpr) * UPW + hw;
+  const int hb = min(hb_raw, nh - 1);  // the last workgroup of a row group may hold fewer heads
+  const bool is_q = hb < Hq;
+  const int h = is_q ? hb : hb - Hq;
+  float* xn = xn_all[hw];
+  const int half = rd >> 1;            // <= 128
+  // table entry e = tid + HD i: row e / half, frequency e % half. Its frequency is loaded first
+  // (vmcnt counts in order), then every row's input, which fly while the table is computed.
+  float fr[TE];
+#pragma unroll
+  for (int i = 0; i < TE; ++i) {
+    const int e = tid + HD * i;
+    fr[i] = half > 0 ? inv_freq[e < R * half ? e % half : 0] : 0.f;
+  }
+  u32x4_t xr[R], vr[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const size_t row = (size_t)min(t0 + r, n - 1) * ldp;  // rows past n re-read row n - 1
+    xr[r] = *reinterpret_cast<const u32x4_t*>(
+        is_q ? qg + row + (size_t)h * 2 * HD + 8 * L : k + row + (size_t)h * HD + 8 * L);
+    vr[r] = is_q ? u32x4_t{0u, 0u, 0u, 0u}
+                 : *reinterpret_cast<const u32x4_t*>(v + row + (size_t)h * HD + 8 * L);
+  }
+  const u32x4_t wr = *reinterpret_cast<const u32x4_t*>((is_q ? qnw : knw) + 8 * L);
+  const int pos0 = pos_ptr[0] + t0;
+#pragma unroll
+  for (int i = 0; i < TE; ++i) {
+    const int e = tid + HD * i;
+    if (e < R * half) {
+      const int r = e / half, f = e - r * half;
+      const RopeCS c = rope_cs_f(pos0 + r, fr[i], rd, f);
+      cst[r][f] = make_float2(c.cs, c.sn);
+    }
+  }
+  lds_barrier();
+  if (hb_raw >= nh) return;
+  float w[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[2 * i] = lo_bf16(wr[i]);
+    w[2 * i + 1] = hi_bf16(wr[i]);
+  }
+  const int base = (tid & ~(HW - 1)) & (WAVE - 1);  // lane 0 of the half-wave
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int t = t0 + r, pos = pos0 + r;
+    if (t >= n) break;  // uniform across the workgroup
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = lo_bf16(xr[r][i]);
+      x[2 * i + 1] = hi_bf16(xr[r][i]);
+    }
+    // sum of squares of the lane's 64-dim group, in wave_sum_fast's order
+    float s[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s[q] = x[q] * x[q];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s[q] = s[q] + dpp<0x1B>(dpp<0x141>(s[q]));  // lane ^ 4: dim ^ 32
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s[q] = s[q] + dpp<0x4E>(s[q]);              // lane ^ 2: dim ^ 16
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s[q] = s[q] + dpp<0xB1>(s[q]);              // lane ^ 1: dim ^ 8
+    float u[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) u[q] = s[q] + s[q + 4];                     // dim ^ 4
+    const float gsum = (u[0] + u[2]) + (u[1] + u[3]);                       // dim ^ 2, then ^ 1
+    const float r0 = __shfl(gsum, base), r1 = __shfl(gsum, base + 8);
+    const float r2 = __shfl(gsum, base + 16), r3 = __shfl(gsum, base + 24);
+    const float total = ((r0 + r1) + r2) + r3;
+    const float inv = 1.0f / sqrtf(total / (float)HD + eps);
+    float xv[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) xv[q] = round_bf16((x[q] * inv) * (1.0f + w[q]));
+    // the half-wave's LDS row: the previous row's partner reads are done before it is rewritten
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    *reinterpret_cast<f32x4_t*>(&xn[8 * L]) = f32x4_t{xv[0], xv[1], xv[2], xv[3]};
+    *reinterpret_cast<f32x4_t*>(&xn[8 * L + 4]) = f32x4_t{xv[4], xv[5], xv[6], xv[7]};
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    float y[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int c = 8 * L + q;
+      if (c < rd) {
+        const float rot = c < half ? -xn[c + half] : xn[c - half];  // rotate_half
+        const float2 e = cst[r][c < half ? c : c - half];
+        y[q] = round_bf16(round_bf16(xv[q] * e.x) + round_bf16(rot * e.y));
+      } else {
+        y[q] = xv[q];
+      }
+    }
+    u32x4_t yo;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      yo[i] = (uint32_t)__builtin_bit_cast(uint16_t, f32_to_bf16(y[2 * i])) |
+              ((uint32_t)__builtin_bit_cast(uint16_t, f32_to_bf16(y[2 * i + 1])) << 16);
+    if (is_q) {
+      *reinterpret_cast<u32x4_t*>(q_out + (size_t)t * Hq * HD + (size_t)h * HD + 8 * L) = yo;
+    } else if (pos >= 0 && pos < max_len) {  // never write outside the cache
+      const size_t dst = ((size_t)h * max_len + pos) * HD + 8 * L;
+      if constexpr (FP8) {
+        uint32_t kw[2], vw[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          kw[i] = 0u;
+          vw[i] = 0u;
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            const int q = 4 * i + b;
+            const float vf = q & 1 ? hi_bf16(vr[r][q >> 1]) : lo_bf16(vr[r][q >> 1]);
+            kw[i] |= (uint32_t)f32_to_fp8(round_bf16(y[q]) * k_inv) << (8 * b);
+            vw[i] |= (uint32_t)f32_to_fp8(vf * v_inv) << (8 * b);
+          }
+        }
+        *reinterpret_cast<uint2*>(static_cast<uint8_t*>(kc) + dst) = make_uint2(kw[0], kw[1]);
+        *reinterpret_cast<uint2*>(static_cast<uint8_t*>(vc) + dst) = make_uint2(vw[0], vw[1]);
+      } else {
+        *reinterpret_cast<u32x4_t*>(static_cast<__bf16*>(kc) + dst) = yo;
+        *reinterpret_cast<u32x4_t*>(static_cast<__bf16*>(vc) + dst) = vr[r];
+      }
+    }
+  }
+}
+
 // Rows per workgroup: one for decode calls, 8 for prefill chunks.
 template <bool FP8>
 static void launch_prep(const void* qg, const void* k, const void* v, long ldp, const void* qnw,
@@ -102,6 +256,22 @@ static void launch_prep(const void* qg, const void* k, const void* v, long ldp, 
   const auto* QW = static_cast<const __bf16*>(qnw);
   const auto* KW = static_cast<const __bf16*>(knw);
   auto* QO = static_cast<__bf16*>(q_out);
+  const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (a16(qg) && a16(k) && a16(v) && a16(qnw) && a16(knw) && a16(q_out) && a16(kc) && a16(vc) &&
+      ldp % 8 == 0) {
+    const unsigned wpr = (Hq + Hkv + 7) / 8;  // workgroups per row group
+    constexpr int PREP_R = 2;  // rows per half-wave for chunks (2048 rows: 1 / 2 / 4 / 8 rows
+                               // per half-wave measured 21.5 / 21.1 / 23.0 / 26.0 us)
+    if (n <= 8)
+      attn_prep_rows_kernel<FP8, 1><<<dim3(n * wpr), dim3(HD), 0, stream>>>(
+          QG, K, V, ldp, QW, KW, inv_freq, pos, QO, kc, vc, n, Hq, Hkv, max_len, rd, eps, k_inv,
+          v_inv);
+    else
+      attn_prep_rows_kernel<FP8, PREP_R><<<dim3((n + PREP_R - 1) / PREP_R * wpr), dim3(HD), 0, stream>>>(
+          QG, K, V, ldp, QW, KW, inv_freq, pos, QO, kc, vc, n, Hq, Hkv, max_len, rd, eps, k_inv,
+          v_inv);
+    return;
+  }
   if (n <= 8)
     attn_prep_kernel<FP8, 1><<<dim3(Hq + Hkv, n), dim3(HD), 0, stream>>>(
         QG, K, V, ldp, QW, KW, inv_freq, pos, QO, kc, vc, n, Hq, max_len, rd, eps, k_inv, v_inv);

@@ -107,7 +107,9 @@ __device__ __forceinline__ float rope_freq(const float* __restrict__ inv_freq, i
 __device__ __forceinline__ RopeCS rope_cs_f(int pos, float freq, int rd, int c) {
   if (c >= rd) return {1.f, 0.f};
   const double angd = (double)((float)pos * freq);  // the fp32 angle, in fp64
-  return {round_bf16((float)cos(angd)), round_bf16((float)sin(angd))};
+  double sn, cs;
+  sincos(angd, &sn, &cs);  // one argument reduction for both
+  return {round_bf16((float)cs), round_bf16((float)sn)};
 }
 __device__ __forceinline__ RopeCS rope_cs(int pos, const float* __restrict__ inv_freq, int rd,
                                           int c) {
