@@ -256,20 +256,18 @@ static void launch_prep(const void* qg, const void* k, const void* v, long ldp, 
   const auto* QW = static_cast<const __bf16*>(qnw);
   const auto* KW = static_cast<const __bf16*>(knw);
   auto* QO = static_cast<__bf16*>(q_out);
+  // Decode calls (<= 8 rows): one row per workgroup (the rows kernel measured 4.1 against 2.5 us
+  // at 1 and 5 rows: its rotary table and barrier sit on a one-row call's critical path).
+  // Chunks with 16-byte aligned rows: attn_prep_rows_kernel; otherwise 8 rows per workgroup.
   const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  if (a16(qg) && a16(k) && a16(v) && a16(qnw) && a16(knw) && a16(q_out) && a16(kc) && a16(vc) &&
-      ldp % 8 == 0) {
+  if (n > 8 && a16(qg) && a16(k) && a16(v) && a16(qnw) && a16(knw) && a16(q_out) && a16(kc) &&
+      a16(vc) && ldp % 8 == 0) {
+    constexpr int R = 2;  // rows per half-wave (2048 rows: 1 / 2 / 4 / 8 measured 21.5 / 21.1 /
+                          // 23.0 / 26.0 us)
     const unsigned wpr = (Hq + Hkv + 7) / 8;  // workgroups per row group
-    constexpr int PREP_R = 2;  // rows per half-wave for chunks (2048 rows: 1 / 2 / 4 / 8 rows
-                               // per half-wave measured 21.5 / 21.1 / 23.0 / 26.0 us)
-    if (n <= 8)
-      attn_prep_rows_kernel<FP8, 1><<<dim3(n * wpr), dim3(HD), 0, stream>>>(
-          QG, K, V, ldp, QW, KW, inv_freq, pos, QO, kc, vc, n, Hq, Hkv, max_len, rd, eps, k_inv,
-          v_inv);
-    else
-      attn_prep_rows_kernel<FP8, PREP_R><<<dim3((n + PREP_R - 1) / PREP_R * wpr), dim3(HD), 0, stream>>>(
-          QG, K, V, ldp, QW, KW, inv_freq, pos, QO, kc, vc, n, Hq, Hkv, max_len, rd, eps, k_inv,
-          v_inv);
+    attn_prep_rows_kernel<FP8, R><<<dim3((n + R - 1) / R * wpr), dim3(HD), 0, stream>>>(
+        QG, K, V, ldp, QW, KW, inv_freq, pos, QO, kc, vc, n, Hq, Hkv, max_len, rd, eps, k_inv,
+        v_inv);
     return;
   }
   if (n <= 8)
