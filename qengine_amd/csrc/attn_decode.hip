@@ -379,9 +379,9 @@ struct PrepIn {
 };
 
 // LDS of the fused prep: the group's q rows (bf16, 16-byte chunks, rows padded by one chunk so the
-// 16 columns a lane group reads hit different banks), per wave: the staged input rows of its items,
-// the two norm weight rows and inv_freq, one 256-float row for the rotate-half exchange; and the
-// rotary cos/sin table of the call's rows.
+// 16 columns a lane group reads hit different banks), per wave: the two norm weight rows and
+// inv_freq, one 256-float row per half-wave for the rotate-half exchange; and the rotary cos/sin
+// table of the call's rows.
 constexpr int FQ_ROW_U4 = ROW_CHUNKS + 1;
 constexpr int PREP_WAVES = 4;
 constexpr int ROPE_TAB = 256;  // n * rd/2 entries, one per thread (the fused path's limit)
@@ -394,10 +394,9 @@ struct PrepShape {
 template <int NT>
 struct FusedLds {
   u32x4_t q[16 * NT][FQ_ROW_U4];
-  u32x4_t stage_x[PREP_WAVES][2 * PrepShape<NT>::PAIRS][ROW_CHUNKS];
   u32x4_t stage_w[PREP_WAVES][2][ROW_CHUNKS];  // qnw, knw
   float stage_f[PREP_WAVES][HD / 2];          // inv_freq (half <= 128)
-  float xn[PREP_WAVES][HD];
+  float xn[PREP_WAVES][2][HD];  // per half-wave item: the normalised row (rotate_half partner)
   float cs[ROPE_TAB], sn[ROPE_TAB];
   u32x4_t knew[FUSED_NEW_ROWS][ROW_CHUNKS];  // the cache rows this workgroup writes, by row t:
   u32x4_t vnew[FUSED_NEW_ROWS][ROW_CHUNKS];  // patched into the tile loaded before the prep
@@ -411,16 +410,15 @@ __device__ __forceinline__ u32x4_t fused_q_lds(int col, int chunk) {
   return reinterpret_cast<const u32x4_t*>(fused_lds_raw)[col * FQ_ROW_U4 + chunk];
 }
 
-// The prep of qe_attn_prep for this workgroup, one row ("item") per wave at a time and no
+// The prep of qe_attn_prep for this workgroup, one row ("item") per half-wave at a time and no
 // workgroup barrier inside an item: items are the ncols q rows of KV head g's group (to LDS, and
 // to q_out from slice 0) and the cache rows pos+t, t in [t_lo, t_hi), that lie in this slice;
-// item i goes to wave i % 4. Lane l holds dims l + 64r (r = 0..3), the prep kernel's thread
-// c = 64r + l, so the four wave butterflies and ((s0 + s1) + s2) + s3 are that kernel's reduction
-// tree, and every output is bit-identical to it.
-// The input rows are loaded with 16-byte loads (lanes 0-31 one row, 32-63 the next), a few per
-// wave, all before the caller's tile prefetch (loads return in order: a later load would wait for
-// the tile, and a wave can have only 63 loads outstanding), and staged through LDS into that layout.
-// The V rows are loaded at the end, only by the workgroup that writes cache rows.
+// items 2P*4 + w and (2P+1)*4 + w go to the two halves of wave w (fused_prep_pair).
+// The input rows are loaded with 16-byte loads (lanes 0-31 one row, 32-63 the next; lane 32h + L
+// holds dims 8L .. 8L+7 of its row, the layout the items compute in), after the norm weights and
+// inv_freq (loads return in order: the rotary table waits only for those) and before the caller's
+// tile prefetch (a later load would wait for the tile, and a wave can have only 63 loads
+// outstanding). The V rows are loaded at the end, only by the workgroup that writes cache rows.
 template <int NT>
 struct PrepRegs {
   u32x4_t x[PrepShape<NT>::PAIRS], w, f;
@@ -432,6 +430,11 @@ __device__ __forceinline__ void fused_prep_load(PrepRegs<NT>& r, const PrepIn& p
   const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
   const int nitems = ncols + (t_hi - t_lo);
   const int hl = lane >> 5, ch = lane & 31;  // row of the pair, 16-byte chunk of the row
+  r.w = reinterpret_cast<const u32x4_t*>(hl ? pin.knw : pin.qnw)[ch];
+  const int half = pin.rd >> 1;  // a multiple of 4 on this path
+  // lanes past the table load (and stage) its last chunk again, so the staging store needs no
+  // branch that the compiler could sink this load into
+  r.f = reinterpret_cast<const u32x4_t*>(pin.inv_freq)[min(lane, half / 4 - 1)];
 #pragma unroll
   for (int P = 0; P < PrepShape<NT>::PAIRS; ++P) {
     int it = (2 * P + hl) * PREP_WAVES + w;
@@ -442,92 +445,124 @@ __device__ __forceinline__ void fused_prep_load(PrepRegs<NT>& r, const PrepIn& p
                             : pin.k + (size_t)t * pin.ldp + (size_t)g * HD;
     r.x[P] = reinterpret_cast<const u32x4_t*>(src)[ch];
   }
-  r.w = reinterpret_cast<const u32x4_t*>(hl ? pin.knw : pin.qnw)[ch];
-  const int half = pin.rd >> 1;  // a multiple of 4 on this path
-  // lanes past the table load (and stage) its last chunk again, so the staging store needs no
-  // branch that the compiler could sink this load into
-  r.f = reinterpret_cast<const u32x4_t*>(pin.inv_freq)[min(lane, half / 4 - 1)];
 }
 
-template <int NT, int K>
-__device__ __forceinline__ void fused_prep_item(const PrepIn& pin, int s, int g, int grp, int Hq,
-                                                int ncols, int nitems, int pos0, int t_lo,
-                                                int max_len, __bf16* kc, __bf16* vc) {
+// One pair of items per wave, one item per half-wave: half hl of wave w takes item
+// (2P + hl) * PREP_WAVES + w, whose input row its lanes loaded themselves (fused_prep_load: lane
+// (hl, ch) holds dims 8ch .. 8ch+7), so the row needs no staging. The sum of squares follows the
+// prep kernel's reduction exactly (attn_prep_rows_kernel: dims c^32, c^16, c^8 in lanes ^4, ^2,
+// ^1, then c^4, c^2, c^1 within the lane, and ((r0 + r1) + r2) + r3 over the four 64-dim groups),
+// so every output is bit-identical to qe_attn_prep. 16-byte LDS and global stores.
+template <int NT, int P>
+__device__ __forceinline__ void fused_prep_pair(const PrepRegs<NT>& r, const PrepIn& pin, int s,
+                                                int g, int grp, int Hq, int ncols, int nitems,
+                                                int pos0, int t_lo, int max_len, __bf16* kc,
+                                                __bf16* vc) {
   FusedLds<NT>& L = fused_lds<NT>();
   const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
-  const int it = K * PREP_WAVES + w;
-  if (it >= nitems) return;  // uniform per wave
+  const int hl = lane >> 5, ch = lane & 31;
+  const int it = (2 * P + hl) * PREP_WAVES + w;
+  if (it >= nitems) return;  // uniform per half-wave
   const int rd = pin.rd, half = rd >> 1;
-  float* xn = L.xn[w];
-  const __bf16* xrow = reinterpret_cast<const __bf16*>(&L.stage_x[w][K][0]);
-  const __bf16* wrow = reinterpret_cast<const __bf16*>(&L.stage_w[w][0][0]);
+  float* xn = L.xn[w][hl];
   const bool isq = it < ncols;
   const int t = isq ? it / grp : t_lo + (it - ncols);
-  float x[4], sr[4];
+  const u32x4_t wr = L.stage_w[w][isq ? 0 : 1][ch];
+  float x[8], wg[8];
 #pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    x[rr] = bf16_to_f32(xrow[lane + 64 * rr]);
-    sr[rr] = wave_sum_fast(x[rr] * x[rr]);
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = lo_bf16(r.x[P][i]);
+    x[2 * i + 1] = hi_bf16(r.x[P][i]);
+    wg[2 * i] = lo_bf16(wr[i]);
+    wg[2 * i + 1] = hi_bf16(wr[i]);
   }
-  const float total = ((sr[0] + sr[1]) + sr[2]) + sr[3];
+  float sq[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) sq[q] = x[q] * x[q];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) sq[q] = sq[q] + dpp<0x1B>(dpp<0x141>(sq[q]));  // lane ^ 4: dim ^ 32
+#pragma unroll
+  for (int q = 0; q < 8; ++q) sq[q] = sq[q] + dpp<0x4E>(sq[q]);              // lane ^ 2: dim ^ 16
+#pragma unroll
+  for (int q = 0; q < 8; ++q) sq[q] = sq[q] + dpp<0xB1>(sq[q]);              // lane ^ 1: dim ^ 8
+  float u[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) u[q] = sq[q] + sq[q + 4];                      // dim ^ 4
+  const float gsum = (u[0] + u[2]) + (u[1] + u[3]);                          // dim ^ 2, then ^ 1
+  const int base = lane & 32;
+  const float r0 = __shfl(gsum, base), r1 = __shfl(gsum, base + 8);
+  const float r2 = __shfl(gsum, base + 16), r3 = __shfl(gsum, base + 24);
+  const float total = ((r0 + r1) + r2) + r3;
   const float inv = 1.0f / sqrtf(total / (float)HD + pin.eps);
-  float xv[4];
+  float xv[8];
 #pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const float wgt = bf16_to_f32(wrow[(isq ? 0 : HD) + lane + 64 * rr]);
-    xv[rr] = round_bf16((x[rr] * inv) * (1.0f + wgt));
-    xn[lane + 64 * rr] = xv[rr];
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  for (int q = 0; q < 8; ++q) xv[q] = round_bf16((x[q] * inv) * (1.0f + wg[q]));
+  // the half-wave's LDS row: the previous pair's partner reads are done before it is rewritten
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  float y[4];
+  *reinterpret_cast<f32x4_t*>(&xn[8 * ch]) = f32x4_t{xv[0], xv[1], xv[2], xv[3]};
+  *reinterpret_cast<f32x4_t*>(&xn[8 * ch + 4]) = f32x4_t{xv[4], xv[5], xv[6], xv[7]};
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  float y[8];
 #pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const int d = lane + 64 * rr;
-    y[rr] = xv[rr];
-    if (d < rd) {
-      const int e = t * half + (d < half ? d : d - half);
-      const float rot = d < half ? -xn[d + half] : xn[d - half];  // rotate_half
-      y[rr] = round_bf16(round_bf16(xv[rr] * L.cs[e]) + round_bf16(rot * L.sn[e]));
+  for (int q = 0; q < 8; ++q) y[q] = xv[q];
+  const int d0 = 8 * ch;
+  if (d0 < rd) {
+    if ((half & 7) == 0) {  // the lane's 8 dims lie on one side of half: 16-byte LDS reads
+      const bool lo = d0 < half;
+      const int e0 = t * half + (lo ? d0 : d0 - half);
+      const float* pp = &xn[lo ? d0 + half : d0 - half];
+      const f32x4_t p[2] = {*reinterpret_cast<const f32x4_t*>(pp),
+                            *reinterpret_cast<const f32x4_t*>(pp + 4)};
+      const f32x4_t c[2] = {*reinterpret_cast<const f32x4_t*>(&L.cs[e0]),
+                            *reinterpret_cast<const f32x4_t*>(&L.cs[e0 + 4])};
+      const f32x4_t sn[2] = {*reinterpret_cast<const f32x4_t*>(&L.sn[e0]),
+                             *reinterpret_cast<const f32x4_t*>(&L.sn[e0 + 4])};
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const float rot = lo ? -p[q >> 2][q & 3] : p[q >> 2][q & 3];  // rotate_half
+        y[q] = round_bf16(round_bf16(xv[q] * c[q >> 2][q & 3]) + round_bf16(rot * sn[q >> 2][q & 3]));
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int d = d0 + q;
+        if (d < rd) {
+          const int e = t * half + (d < half ? d : d - half);
+          const float rot = d < half ? -xn[d + half] : xn[d - half];  // rotate_half
+          y[q] = round_bf16(round_bf16(xv[q] * L.cs[e]) + round_bf16(rot * L.sn[e]));
+        }
+      }
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // xn reads done before the next item
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  u32x4_t yo;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    yo[i] = (uint32_t)__builtin_bit_cast(uint16_t, f32_to_bf16(y[2 * i])) |
+            ((uint32_t)__builtin_bit_cast(uint16_t, f32_to_bf16(y[2 * i + 1])) << 16);
   if (isq) {
     const int head = g * grp + it % grp;
-    __bf16* qrow = reinterpret_cast<__bf16*>(&L.q[0][0]) + it * FQ_ROW_U4 * 8;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const __bf16 yb = f32_to_bf16(y[rr]);
-      qrow[lane + 64 * rr] = yb;
-      if (s == 0) pin.q_out[(size_t)t * Hq * HD + (size_t)head * HD + lane + 64 * rr] = yb;
-    }
+    L.q[it][ch] = yo;
+    if (s == 0)
+      *reinterpret_cast<u32x4_t*>(pin.q_out + (size_t)t * Hq * HD + (size_t)head * HD + 8 * ch) = yo;
   } else {
-    const size_t dst = ((size_t)g * max_len + (pos0 + t)) * HD;
-    const __bf16* vrow = pin.v + (size_t)t * pin.ldp + (size_t)g * HD;
-    __bf16* kn = reinterpret_cast<__bf16*>(&L.knew[t][0]);
-    __bf16* vn = reinterpret_cast<__bf16*>(&L.vnew[t][0]);
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const __bf16 kb = f32_to_bf16(y[rr]), vb = vrow[lane + 64 * rr];  // v bit for bit
-      kc[dst + lane + 64 * rr] = kb;
-      vc[dst + lane + 64 * rr] = vb;
-      kn[lane + 64 * rr] = kb;
-      vn[lane + 64 * rr] = vb;
-    }
+    const size_t dst = ((size_t)g * max_len + (pos0 + t)) * HD + 8 * ch;
+    const u32x4_t vb = *reinterpret_cast<const u32x4_t*>(
+        pin.v + (size_t)t * pin.ldp + (size_t)g * HD + 8 * ch);  // v bit for bit
+    *reinterpret_cast<u32x4_t*>(kc + dst) = yo;
+    *reinterpret_cast<u32x4_t*>(vc + dst) = vb;
+    L.knew[t][ch] = yo;
+    L.vnew[t][ch] = vb;
   }
 }
 
-// The loaded input rows into this wave's LDS staging area (waits for the loads).
+// The norm weights and inv_freq into this wave's LDS staging area (waits for those two loads).
 template <int NT>
 __device__ __forceinline__ void fused_prep_stage(const PrepRegs<NT>& r, const PrepIn& pin) {
   FusedLds<NT>& L = fused_lds<NT>();
   const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
   const int hl = lane >> 5, ch = lane & 31, half = pin.rd >> 1;
-#pragma unroll
-  for (int P = 0; P < PrepShape<NT>::PAIRS; ++P) L.stage_x[w][2 * P + hl][ch] = r.x[P];
   L.stage_w[w][hl][ch] = r.w;
   reinterpret_cast<u32x4_t*>(L.stage_f[w])[min(lane, half / 4 - 1)] = r.f;  // same bits per slot
 }
@@ -553,13 +588,15 @@ __device__ __forceinline__ void fused_prep_table(const PrepIn& pin, int n, int p
 // After fused_prep_table. Ends with a workgroup barrier after which the q rows are readable in
 // LDS and, in the workgroup that writes cache rows, those writes have completed (so the waves'
 // later tile loads see them).
-template <int NT, int... Ks>
-__device__ __forceinline__ void fused_prep_compute(const PrepIn& pin, int s, int g, int grp, int n,
-                                                   int Hq, int ncols, int pos0, int t_lo,
-                                                   int t_hi, int max_len, __bf16* kc, __bf16* vc,
-                                                   std::integer_sequence<int, Ks...>) {
+template <int NT, int... Ps>
+__device__ __forceinline__ void fused_prep_compute(const PrepRegs<NT>& r, const PrepIn& pin, int s,
+                                                   int g, int grp, int n, int Hq, int ncols,
+                                                   int pos0, int t_lo, int t_hi, int max_len,
+                                                   __bf16* kc, __bf16* vc,
+                                                   std::integer_sequence<int, Ps...>) {
   const int nitems = ncols + (t_hi - t_lo);
-  (fused_prep_item<NT, Ks>(pin, s, g, grp, Hq, ncols, nitems, pos0, t_lo, max_len, kc, vc), ...);
+  (fused_prep_pair<NT, Ps>(r, pin, s, g, grp, Hq, ncols, nitems, pos0, t_lo, max_len, kc, vc),
+   ...);
   if (t_hi > t_lo)
     __syncthreads();  // release: the cache rows are written before any wave loads them
   else
@@ -657,18 +694,22 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
     fused_prep_stage<NT>(pr, pin);
     fused_prep_table<NT>(pin, n, pos0);
     // The wave's first tile does not depend on the prep (rows the prep writes are patched in
-    // after it, fused_patch_tile): its loads go out once the prep's inputs are staged (so no wait
-    // for those inputs can also wait for the tile) and the rotary table, which one wave computes
-    // for all, is done, and land while the items run.
+    // after it, fused_place_tile): its loads go out once the rotary table, which one wave
+    // computes for all, is done and the input rows have arrived (so no wait for those rows can
+    // also wait for the tile), and land while the items run.
     const Pass P0 = attendA ? PA : PB;
     const int pf_p0 = P0.beg + w * TILE;
     pf = attend && pf_p0 < P0.end;
     __builtin_amdgcn_sched_barrier(0);
+    // The input rows arrived during the table; waiting for them here, before the conditional
+    // tile loads, keeps the compiler from waiting for the tile too where the items read them.
+#pragma unroll
+    for (int P = 0; P < PrepShape<NT>::PAIRS; ++P) asm volatile("" ::"v"(pr.x[P]));
     if (pf) load_tile_regs(kpf, buf, pass_rsrc(P0, kc), pass_rsrc(P0, vc), pf_p0, lane, c, g4);
     __builtin_amdgcn_sched_barrier(0);
-    fused_prep_compute<NT>(pin, s, g, grp, n, Hq, ncols, pos0, t_lo, t_hi, max_len,
+    fused_prep_compute<NT>(pr, pin, s, g, grp, n, Hq, ncols, pos0, t_lo, t_hi, max_len,
                            const_cast<__bf16*>(kc), const_cast<__bf16*>(vc),
-                           std::make_integer_sequence<int, PrepShape<NT>::MAXI>{});
+                           std::make_integer_sequence<int, PrepShape<NT>::PAIRS>{});
     if (!attend) return;  // slice 0 beyond every attended position: q_out written, nothing else
 #pragma unroll
     for (int ct = 0; ct < NT; ++ct) {
@@ -746,6 +787,13 @@ attn_partials_kernel(const __bf16* __restrict__ q, const __bf16* kc, const __bf1
         wait_and_compute<NT>(buf, ks_lds, p0, P.Lmin, Lcol, qb, scale_log2, c, g4, m, l, acc);
         p0 += STEP;
       }
+      // Where no tile was loaded before the prep, the compiler, which cannot tie this branch to
+      // the prefetch's, counts those loads as pending: uses of the registers here take its wait
+      // before the loop, not among the tile loop's K loads (no wait at run time on either path).
+#pragma unroll
+      for (int j = 0; j < 16; ++j) asm volatile("" ::"v"(kpf.k[j]));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) asm volatile("" ::"v"(buf.v[e][0]), "v"(buf.v[e][1]));
       const TileLanes tl(lane);
       for (; p0 < P.end; p0 += STEP) {
         load_tile(buf, ks_s, tile_rsrc(kbase, p0, P.end, HD * 2),

@@ -8,9 +8,10 @@ with inv_freq built on the CPU in fp32 and moved (engine.py:409-410), per-layer 
 [Hkv, max_len, 256] (engine.py:419) and a shared q / part_o / part_ml scratch (engine.py:405-408).
 GatedAttention owns the same buffers and issues the same work, by default as the reference's two
 calls; fused=True issues the fused attn_prep_decode instead (two launches instead of three,
-bit-identical results, but about 1 us slower per layer-call on gfx950 because the prep phase
-delays every workgroup's first KV tile). It allocates only at construction, so a pass can be
-captured in a hipGraph.
+bit-identical results; on gfx950 up to 0.7 us faster per layer-call for one row on caches up to
+8k positions, up to 1.2 us slower for two rows and at 16k, where the fused kernel's single-slot
+KV tile loop costs more than the launch it saves). It allocates only at construction, so a pass
+can be captured in a hipGraph.
 """
 from __future__ import annotations
 
