@@ -100,8 +100,10 @@ attn_prep_kernel(const __bf16* __restrict__ qg, const __bf16* __restrict__ k,
 // cos/sin, the kernel's most expensive step) are computed once per workgroup into an LDS table
 // (one workgroup barrier); the rotate_half partner goes through the half-wave's own LDS row.
 // Needs 16-byte aligned rows (checked by the launcher; otherwise attn_prep_kernel runs).
+// The rotary lanes read the rotate_half partner and cos/sin as 16-byte vectors (8 consecutive
+// dims of one side of rd/2; scalar reads where rd/2 is not a multiple of 8).
 // 2048-row chunk at 24 Q / 4 KV heads, same box: 33.4 us for attn_prep_kernel<false, 8>, about
-// 21 us here (the launcher's R).
+// 18.5 us here (the launcher's R; 20.7 with scalar rotary reads).
 template <bool FP8, int R>
 __global__ void __launch_bounds__(HD)
 attn_prep_rows_kernel(const __bf16* __restrict__ qg, const __bf16* __restrict__ k,
@@ -113,8 +115,8 @@ attn_prep_rows_kernel(const __bf16* __restrict__ qg, const __bf16* __restrict__ 
   constexpr int HW = 32;                   // lanes per head
   constexpr int UPW = HD / HW;             // heads per workgroup
   constexpr int TE = (R * (HD / 2) + HD - 1) / HD;  // table entries per thread, at most
-  __shared__ float xn_all[UPW][HD];        // per half-wave: the normalised row
-  __shared__ float2 cst[R][HD / 2];        // cos/sin of the rows' rd/2 frequencies
+  __shared__ __attribute__((aligned(16))) float xn_all[UPW][HD];  // per half-wave: normalised row
+  __shared__ __attribute__((aligned(16))) float2 cst[R][HD / 2];  // cos/sin of rd/2 frequencies
   const int tid = threadIdx.x, hw = tid / HW, L = tid & (HW - 1);
   const int nh = Hq + Hkv, wpr = (nh + UPW - 1) / UPW;  // workgroups per row group
   const int grp = blockIdx.x / wpr, t0 = grp * R;
@@ -201,14 +203,32 @@ attn_prep_rows_kernel(const __bf16* __restrict__ qg, const __bf16* __restrict__ 
     __builtin_amdgcn_wave_barrier();
     float y[8];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int c = 8 * L + q;
-      if (c < rd) {
-        const float rot = c < half ? -xn[c + half] : xn[c - half];  // rotate_half
-        const float2 e = cst[r][c < half ? c : c - half];
-        y[q] = round_bf16(round_bf16(xv[q] * e.x) + round_bf16(rot * e.y));
+    for (int q = 0; q < 8; ++q) y[q] = xv[q];
+    const int c0 = 8 * L;
+    if (c0 < rd) {
+      if ((half & 7) == 0) {  // the lane's 8 dims lie on one side of half: 16-byte LDS reads
+        const bool lo = c0 < half;
+        const float* pp = &xn[lo ? c0 + half : c0 - half];
+        const f32x4_t p[2] = {*reinterpret_cast<const f32x4_t*>(pp),
+                              *reinterpret_cast<const f32x4_t*>(pp + 4)};
+        const f32x4_t* ep = reinterpret_cast<const f32x4_t*>(&cst[r][lo ? c0 : c0 - half]);
+        const f32x4_t e[4] = {ep[0], ep[1], ep[2], ep[3]};  // (cos, sin) of 8 frequencies
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const float rot = lo ? -p[q >> 2][q & 3] : p[q >> 2][q & 3];  // rotate_half
+          const float cs = e[q >> 1][2 * (q & 1)], sn = e[q >> 1][2 * (q & 1) + 1];
+          y[q] = round_bf16(round_bf16(xv[q] * cs) + round_bf16(rot * sn));
+        }
       } else {
-        y[q] = xv[q];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int c = c0 + q;
+          if (c < rd) {
+            const float rot = c < half ? -xn[c + half] : xn[c - half];  // rotate_half
+            const float2 e = cst[r][c < half ? c : c - half];
+            y[q] = round_bf16(round_bf16(xv[q] * e.x) + round_bf16(rot * e.y));
+          }
+        }
       }
     }
     u32x4_t yo;
@@ -262,8 +282,8 @@ static void launch_prep(const void* qg, const void* k, const void* v, long ldp, 
   const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   if (n > 8 && a16(qg) && a16(k) && a16(v) && a16(qnw) && a16(knw) && a16(q_out) && a16(kc) &&
       a16(vc) && ldp % 8 == 0) {
-    constexpr int R = 2;  // rows per half-wave (2048 rows: 1 / 2 / 4 / 8 measured 21.5 / 21.1 /
-                          // 23.0 / 26.0 us)
+    constexpr int R = 2;  // rows per half-wave (2048 rows: 1 / 2 / 3 / 4 measured 18.9 / 18.4 /
+                          // 19.3 / 19.1 us)
     const unsigned wpr = (Hq + Hkv + 7) / 8;  // workgroups per row group
     attn_prep_rows_kernel<FP8, R><<<dim3((n + R - 1) / R * wpr), dim3(HD), 0, stream>>>(
         QG, K, V, ldp, QW, KW, inv_freq, pos, QO, kc, vc, n, Hq, Hkv, max_len, rd, eps, k_inv,
