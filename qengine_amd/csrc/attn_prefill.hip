@@ -24,11 +24,12 @@
 //    in one register class across iterations.
 //  * Epilogue: O / l rounded to bf16, times bf16(sigmoid(gate)), 8-byte stores.
 //  * At GQA 6 (bf16 and fp8 caches), attn_prefill_bal_kernel runs the same per-wave code in a
-//    layout that balances the causal triangle: 12 waves (three per SIMD) own one KV head and the
-//    16-row blocks j and nb-1-j of all six q heads, so every workgroup carries about the same
-//    work and the grid is one round of workgroups (config 5: 256). Same bits as the 8-wave
-//    kernel; 222 -> 212 us at config 5 (same-box A/B). On the fp8 cache it replaced the 8-wave
-//    kernel at GQA 6: 290 -> 243 us.
+//    layout that balances the causal triangle: 12 waves (three per SIMD) of one KV head own
+//    three quads of (16-row block, q head) units, four units of one length per quad, one unit of
+//    each quad per SIMD; the quads of a workgroup mix lengths so that every workgroup carries
+//    about the same work, and the grid is one round of workgroups (config 5: 256). Same bits as
+//    the 8-wave kernel. Its first form (blocks j and nb-1-j, one q head per wave): 222 -> 212 us
+//    at config 5 (same-box A/B); on the fp8 cache it replaced the 8-wave kernel: 290 -> 243 us.
 //  * The file is compiled with LLVM's max-ILP machine scheduler. Under the default
 //    (occupancy-first) scheduler the tile loop kept one LDS operand read in flight and waited
 //    for it before every MFMA; max-ILP interleaves the two S^T accumulation chains and keeps two
@@ -414,10 +415,50 @@ attn_prefill_bal_kernel(const __bf16* __restrict__ q, const void* __restrict__ k
   }
   const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
   const int c = lane & 15, g4 = lane >> 4;
-  const int half = w / BAL_GRP, h = g * BAL_GRP + w % BAL_GRP;
-  const int bl = jp, bh = nb - 1 - jp;
-  const int blk = half ? bh : bl;
-  const bool wave_live = !(half && bh == bl);  // odd block count: the middle pair has one block
+  // Units (16-row block, q head) in quads of four of (nearly) the same length: heads 0-3 of block
+  // b, and heads 4-5 of blocks 2m and 2m + 1. Quad rank r = 3m + type runs in length order:
+  // type 0 = block 2m, 1 = block 2m + 1, 2 = the heads 4-5 quad of both. Each workgroup takes
+  // three ranks (P = npairs workgroups per KV head), and wave w = 4k + s runs unit s of its k-th
+  // quad. Wave w runs on SIMD w mod 4, so every SIMD holds one unit of each quad: the same
+  // lengths on all four at every tile step. (Pairs of blocks j, nb-1-j with one head per wave
+  // left the heavy block's six waves 2 / 2 / 1 / 1 on the SIMDs past the light block's end: the
+  // workgroups of block 127 ran 13% longer than those of block 64 at config 5.) Per-workgroup
+  // timings put a tile step at ~0.74 / 0.66 / 0.48 us with 3 / 2 / 1 waves per SIMD, so how
+  // the lengths are grouped matters beyond their sum. Measured at config 5 (same bits): bf16
+  // cache, ranks jp, P + p2(jp), 2P + p3(jp) with jp + p2 + p3 within one of a constant, 162.2 ->
+  // 158.1 us (2jp, 2jp + 1, 3P - 1 - jp: 159.0); fp8 cache, ranks 2jp, 2jp + 1 (two short or
+  // two mid-length quads) and 3P - 1 - jp (the longest left), 193.5 -> 183.6 us (the other:
+  // 187.4). Each unit's arithmetic is unchanged.
+  const int P = npairs;
+  auto triple_rank = [&](int k) __attribute__((always_inline)) {
+    if constexpr (KV8) return k < 2 ? 2 * jp + k : 3 * P - 1 - jp;
+    const int Q = P - (P & 1), hh = Q / 2;  // odd P: the last workgroup takes ranks Q, 2Q+1, 3Q+2
+    int p2, p3;
+    if (jp == Q) {
+      p2 = Q;
+      p3 = Q;
+    } else if (jp < hh) {
+      p2 = hh + jp;
+      p3 = Q - 2 - 2 * jp;
+    } else {
+      p2 = jp - hh;
+      p3 = 2 * Q - 1 - 2 * jp;
+    }
+    return k == 0 ? jp : k == 1 ? P + p2 : 2 * P + p3;
+  };
+  // the last live block of a quad (-1: none)
+  auto quad_top = [&](int rank) __attribute__((always_inline)) {
+    const int m = rank / 3, type = rank - 3 * m;
+    const int b = type < 2 ? 2 * m + type : 2 * m + 1;
+    return min(b, nb - 1) >= 2 * m + (type == 1) ? min(b, nb - 1) : -1;
+  };
+  const int wu = __builtin_amdgcn_readfirstlane(w);  // the unit is wave-uniform (scalar)
+  const int rank = triple_rank(wu >> 2), s = wu & 3;
+  const int qm = rank / 3, qtype = rank - 3 * qm;
+  const int blk = qtype < 2 ? 2 * qm + qtype : 2 * qm + (s >> 1);
+  const int h = g * BAL_GRP + (qtype < 2 ? s : 4 + (s & 1));
+  const bool wave_live = blk < nb;
+  const int btop = max(quad_top(triple_rank(0)), max(quad_top(triple_rank(1)), quad_top(triple_rank(2))));
   const int pos0 = pos_ptr[0];
 
   __shared__ __attribute__((aligned(256))) u32x4_t lds[STAGES * STAGE_U4];  // 128 KB
@@ -435,8 +476,8 @@ attn_prefill_bal_kernel(const __bf16* __restrict__ q, const void* __restrict__ k
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) qb[0][ks] = as_bf16x8(u32x4_t{0u, 0u, 0u, 0u});
   }
-  // the workgroup's longest attended prefix is the heavy block's last row
-  const int last_row = min(bh * 16 + 16, T) - 1;
+  // the workgroup's longest attended prefix is its last live block's last row
+  const int last_row = min(btop * 16 + 16, T) - 1;
   const int Lwg = min(pos0 + last_row + 1, max_len);
   const int Lwave = wave_live ? min(pos0 + min(blk * 16 + 16, T), max_len) : 0;
   const int Lmin = min(pos0 + blk * 16 + 1, max_len);
