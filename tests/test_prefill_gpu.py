@@ -34,6 +34,8 @@ def run_prefill(C, q, kc, vc, pos, qg):
     (12, 2, 16, 0, 16),        # GQA 6, one 16-row block (the balanced layout's half pair)
     (24, 4, 17, 3, 30),        # GQA 6, two blocks, the second ragged
     (6, 1, 48, 700, 760),      # GQA 6, one KV head, three blocks
+    (24, 4, 150, 30, 180),     # GQA 6, 10 blocks: an odd number (5) of workgroups per KV head
+    (6, 1, 80, 0, 80),         # GQA 6, 5 blocks (3 workgroups, the last block's quad part-empty)
 ])
 def test_prefill_matches_oracle(native, hq, hkv, T, pos, max_len):
     g = gen(hq * 1000 + T)
