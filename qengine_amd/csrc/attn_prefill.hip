@@ -424,27 +424,19 @@ attn_prefill_bal_kernel(const __bf16* __restrict__ q, const void* __restrict__ k
   // left the heavy block's six waves 2 / 2 / 1 / 1 on the SIMDs past the light block's end: the
   // workgroups of block 127 ran 13% longer than those of block 64 at config 5.) Per-workgroup
   // timings put a tile step at ~0.74 / 0.66 / 0.48 us with 3 / 2 / 1 waves per SIMD, so how
-  // the lengths are grouped matters beyond their sum. Measured at config 5 (same bits): bf16
-  // cache, ranks jp, P + p2(jp), 2P + p3(jp) with jp + p2 + p3 within one of a constant, 162.2 ->
-  // 158.1 us (2jp, 2jp + 1, 3P - 1 - jp: 159.0); fp8 cache, ranks 2jp, 2jp + 1 (two short or
-  // two mid-length quads) and 3P - 1 - jp (the longest left), 193.5 -> 183.6 us (the other:
-  // 187.4). Each unit's arithmetic is unchanged.
+  // the lengths are grouped matters beyond their sum. Measured at config 5 (same bits; one-process
+  // A/Bs of library builds, us per call): ranks jp, P + p2(jp), 2P + p3(jp) with jp + p2 + p3
+  // within one of a constant took bf16 162.2 -> 158.1 and fp8 193.5 -> 187.4 against the pairs;
+  // 2jp, 2jp + 1 and 3P - 1 - jp (two short or two mid-length quads with the longest left) bf16
+  // 159.0, fp8 183.6; on another box P - 1 - jp, 2P - 1 - jp, 2P + jp (the tiers matched in
+  // opposite order) bf16 158.9 against 161.3 for the first, fp8 188.6 against 183.9 for the second,
+  // and jp, 2P - 1 - jp, 2P + jp bf16 162.6, fp8 190.8. So the bf16 instance takes the opposite
+  // tiers and the fp8 one (whose loading waves also convert each tile) the second rule. Each
+  // unit's arithmetic is unchanged.
   const int P = npairs;
   auto triple_rank = [&](int k) __attribute__((always_inline)) {
     if constexpr (KV8) return k < 2 ? 2 * jp + k : 3 * P - 1 - jp;
-    const int Q = P - (P & 1), hh = Q / 2;  // odd P: the last workgroup takes ranks Q, 2Q+1, 3Q+2
-    int p2, p3;
-    if (jp == Q) {
-      p2 = Q;
-      p3 = Q;
-    } else if (jp < hh) {
-      p2 = hh + jp;
-      p3 = Q - 2 - 2 * jp;
-    } else {
-      p2 = jp - hh;
-      p3 = 2 * Q - 1 - 2 * jp;
-    }
-    return k == 0 ? jp : k == 1 ? P + p2 : 2 * P + p3;
+    return k == 0 ? P - 1 - jp : k == 1 ? 2 * P - 1 - jp : 2 * P + jp;
   };
   // the last live block of a quad (-1: none)
   auto quad_top = [&](int rank) __attribute__((always_inline)) {
