@@ -422,9 +422,9 @@ attn_prefill_bal_kernel(const __bf16* __restrict__ q, const void* __restrict__ k
   // quad. Wave w runs on SIMD w mod 4, so every SIMD holds one unit of each quad: the same
   // lengths on all four at every tile step. (Pairs of blocks j, nb-1-j with one head per wave
   // left the heavy block's six waves 2 / 2 / 1 / 1 on the SIMDs past the light block's end: the
-  // workgroups of block 127 ran 13% longer than those of block 64 at config 5.) Per-workgroup
-  // timings put a tile step at ~0.74 / 0.66 / 0.48 us with 3 / 2 / 1 waves per SIMD, so how
-  // the lengths are grouped matters beyond their sum. Measured at config 5 (same bits; one-process
+  // workgroups of block 127 ran 13% longer than those of block 64 at config 5.) A tile step
+  // costs more, per unit, with fewer waves on the SIMD, so how the lengths are grouped matters
+  // beyond their sum; the rules were chosen by measurement. Measured at config 5 (same bits; one-process
   // A/Bs of library builds, us per call): ranks jp, P + p2(jp), 2P + p3(jp) with jp + p2 + p3
   // within one of a constant took bf16 162.2 -> 158.1 and fp8 193.5 -> 187.4 against the pairs;
   // 2jp, 2jp + 1 and 3P - 1 - jp (two short or two mid-length quads with the longest left) bf16
