@@ -372,7 +372,12 @@ __device__ __forceinline__ void run_tiles_bal(int j0, int j1, int Lwave, u32x4_t
 
 // run_tiles_bal on the fp8 cache: the fp8 ring and the double-buffered bf16 pair of
 // run_tiles8, loaded and converted by the first 8 waves (LOAD; 512 threads, one 16-byte chunk of
-// K and of V each).
+// K and of V each), one tile ahead: iteration j converts tile j + 1 into pair (j + 1) % 2 while
+// every wave computes tile j from pair j % 2, so one barrier per tile serves both (the tile
+// converted before the barrier of iteration j is tile j). Tile j's fp8 stage is free once it has
+// been converted, so iteration j refills it with tile j + STAGES: loads still run STAGES - 1
+// iterations ahead of their conversion. Same bits; config 5 fp8 188.3 -> 182.9 us with the rank
+// rule of the bf16 instance (the convert-then-barrier-then-compute loop: 188.3 / 186.5).
 template <bool SPLIT, bool MASK, bool LOAD>
 __device__ __forceinline__ void run_tiles_bal8(int j0, int j1, int Lwave, u32x4_t* lds,
                                                __amdgpu_buffer_rsrc_t krs,
@@ -383,13 +388,13 @@ __device__ __forceinline__ void run_tiles_bal8(int j0, int j1, int Lwave, u32x4_
   u32x4_t* bfp = lds + STAGES * STAGE8_U4;
   for (int j = j0; j < j1; ++j) {
     const int p0 = j * BN;
-    vmcnt_wait<LOADS_PER_TILE8 * (AHEAD - 1)>();  // this wave's loads of tile j are done
-    __syncthreads();  // ... and every wave's; tile j-1's fp8 stage and pair j % 2 are free
+    vmcnt_wait<LOADS_PER_TILE8 * (STAGES - 2)>();  // this wave's loads of tile j + 1 are done
+    // ... and every wave's; bf16 tile j is complete, tile j's fp8 stage and pair (j + 1) % 2 free
+    __syncthreads();
     if (LOAD) {
-      issue_tile8(lds + ((j + AHEAD) % STAGES) * STAGE8_U4, krs, vrs, p0 + AHEAD * BN, w, lane);
-      convert_tile8(lds + (j % STAGES) * STAGE8_U4, bfp + (j & 1) * STAGE_U4);
+      issue_tile8(lds + (j % STAGES) * STAGE8_U4, krs, vrs, p0 + STAGES * BN, w, lane);
+      convert_tile8(lds + ((j + 1) % STAGES) * STAGE8_U4, bfp + ((j + 1) & 1) * STAGE_U4);
     }
-    lds_barrier();  // the bf16 tile is complete
     if (p0 >= Lwave) continue;
     const u32x4_t* bf = bfp + (j & 1) * STAGE_U4;
     tile_math_bal<SPLIT, MASK>(bf, bf + TILE_U4, p0, lane, c, g4, qb, Lcol, scale_log2, st);
@@ -424,18 +429,19 @@ attn_prefill_bal_kernel(const __bf16* __restrict__ q, const void* __restrict__ k
   // left the heavy block's six waves 2 / 2 / 1 / 1 on the SIMDs past the light block's end: the
   // workgroups of block 127 ran 13% longer than those of block 64 at config 5.) A tile step
   // costs more, per unit, with fewer waves on the SIMD, so how the lengths are grouped matters
-  // beyond their sum; the rules were chosen by measurement. Measured at config 5 (same bits; one-process
-  // A/Bs of library builds, us per call): ranks jp, P + p2(jp), 2P + p3(jp) with jp + p2 + p3
-  // within one of a constant took bf16 162.2 -> 158.1 and fp8 193.5 -> 187.4 against the pairs;
+  // beyond their sum; the rule was chosen by measurement. Measured at config 5 (same bits;
+  // one-process A/Bs of library builds, us per call): ranks jp, P + p2(jp), 2P + p3(jp) with
+  // jp + p2 + p3 within one of a constant took bf16 162.2 -> 158.1 and fp8 193.5 -> 187.4 against
+  // the pairs;
   // 2jp, 2jp + 1 and 3P - 1 - jp (two short or two mid-length quads with the longest left) bf16
   // 159.0, fp8 183.6; on another box P - 1 - jp, 2P - 1 - jp, 2P + jp (the tiers matched in
   // opposite order) bf16 158.9 against 161.3 for the first, fp8 188.6 against 183.9 for the second,
-  // and jp, 2P - 1 - jp, 2P + jp bf16 162.6, fp8 190.8. So the bf16 instance takes the opposite
-  // tiers and the fp8 one (whose loading waves also convert each tile) the second rule. Each
+  // and jp, 2P - 1 - jp, 2P + jp bf16 162.6, fp8 190.8. So the opposite tiers are taken. (The fp8
+  // instance kept the second rule while its loop converted each tile between two barriers;
+  // with the conversion one tile ahead the opposite tiers measured 182.9 against 186.5 us.) Each
   // unit's arithmetic is unchanged.
   const int P = npairs;
   auto triple_rank = [&](int k) __attribute__((always_inline)) {
-    if constexpr (KV8) return k < 2 ? 2 * jp + k : 3 * P - 1 - jp;
     return k == 0 ? P - 1 - jp : k == 1 ? 2 * P - 1 - jp : 2 * P + jp;
   };
   // the last live block of a quad (-1: none)
@@ -492,13 +498,18 @@ attn_prefill_bal_kernel(const __bf16* __restrict__ q, const void* __restrict__ k
   if (w < WAVES) {
     if constexpr (KV8) {
 #pragma unroll
-      for (int a = 0; a < AHEAD; ++a)
+      for (int a = 0; a < STAGES; ++a)
         issue_tile8(lds + a * STAGE8_U4, krs, vrs, a * BN, w, lane);
+      vmcnt_wait<LOADS_PER_TILE8 * (STAGES - 1)>();  // this wave's loads of tile 0 are done
     } else {
 #pragma unroll
       for (int a = 0; a < BAL_AHEAD; ++a)
         issue_tile(lds + a * STAGE_U4, krs, vrs, a * BN, w, lane);
     }
+  }
+  if constexpr (KV8) {  // the fp8 loop converts one tile ahead: tile 0 here
+    __syncthreads();     // every wave's loads of tile 0 are done
+    if (w < WAVES) convert_tile8(lds, lds + STAGES * STAGE8_U4);
   }
   // one branch-free loop body per (split, mask) case
   auto run = [&](auto sp, auto mk, int j0, int j1) __attribute__((always_inline)) {
