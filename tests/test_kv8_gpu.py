@@ -183,10 +183,12 @@ def run_prefill(C, q, qg, kc, vc, pos, fp8=False, ks=1.0, vs=1.0):
 
 
 @pytest.mark.parametrize("hq,hkv,T,pos", [(24, 4, 200, 300), (8, 2, 129, 0), (24, 4, 64, 2000),
-                                          (16, 1, 300, 700)])
+                                          (16, 1, 300, 700), (8, 8, 1, 0), (6, 6, 17, 31),
+                                          (24, 4, 1, 0)])
 def test_prefill_fp8_scale_one_equals_bf16(native, hq, hkv, T, pos):
     """Chunked prefill over the fp8 cache with scales of 1 equals attn_prefill over the
-    dequantized bf16 cache bit for bit (short rows included: they take the hi + lo P split)."""
+    dequantized bf16 cache bit for bit (short rows included: they take the hi + lo P split; one
+    row at position 0 is one tile, so the tile converted ahead lies past the cache)."""
     case = decode_case(seed=T + pos, hq=hq, hkv=hkv, pos=pos, n=T, max_len=pos + T + 9)
     kc8, vc8 = quantize_cache(case.kc, 1.0), quantize_cache(case.vc, 1.0)
     kd = K8.dequantize(kc8.view(torch.uint8), 1.0).to(BF)
