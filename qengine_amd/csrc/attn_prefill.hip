@@ -158,13 +158,14 @@ __device__ __forceinline__ void convert_tile8(const u32x4_t* stage, u32x4_t* bf)
   bf[TILE_U4 + r * ROW_CHUNKS + ((q + 1 - p) ^ tile::v_swz(r))] = fp8x8_to_bf16x8(vb);
 }
 
-// run_tiles for the fp8 cache, converting one tile ahead: iteration j converts tile j + 1 into
-// bf16 pair (j + 1) % 2 (whose previous tile, j - 1, every wave finished before this iteration's
-// barrier) while every wave computes tile j from pair j % 2, so one barrier per tile orders both.
-// Tile j's fp8 stage is free once converted, so iteration j refills it with tile j + STAGES and
-// loads still run STAGES - 1 iterations ahead of their conversion. (Converting tile j between two
-// barriers and then computing it: config 5 shapes at GQA 4 / 8 277.8 / 178.1 us against 264.5 /
-// 169.3, same bits.)
+// run_tiles for the fp8 cache, converting one tile ahead: iteration j computes tile j from bf16
+// pair j % 2, then converts tile j + 1 into pair (j + 1) % 2 (whose previous tile, j - 1, every
+// wave finished before this iteration's barrier), so one barrier per tile orders both. Tile j's
+// fp8 stage is free once converted, so iteration j refills it with tile j + STAGES and loads
+// still run STAGES - 1 iterations ahead of their conversion. Same bits throughout; config 5
+// shapes at GQA 4 / 8: converting tile j between two barriers, then computing it, 277.8 / 178.1
+// us; one barrier, converting before the arithmetic 264.5 / 169.3 (266.3 / 169.5 on another
+// box); after it 257.9 / 163.3.
 template <bool SPLIT, bool MASK>
 __device__ __forceinline__ void run_tiles8(int j0, int j1, int Lwave, u32x4_t* lds,
                                            __amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
@@ -178,15 +179,16 @@ __device__ __forceinline__ void run_tiles8(int j0, int j1, int Lwave, u32x4_t* l
     // ... and every wave's; bf16 tile j is complete, tile j's fp8 stage and pair (j + 1) % 2 free
     __syncthreads();
     issue_tile8(lds + (j % STAGES) * STAGE8_U4, krs, vrs, p0 + STAGES * BN, w, lane);
+    if (p0 < Lwave) {
+      const u32x4_t* bf = bfp + (j & 1) * STAGE_U4;
+      f32x4_t sacc[NT][2];
+      tile::qk_tile<NT, NT == 1, SG_LEAD>(bf, qb, c, g4, sacc);
+      u32x4_t pb_hi[NT], pb_lo[NT];
+      tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc, pb_hi,
+                                          pb_lo);
+      tile::pv_tile_tr<NT, SPLIT, NT == 1, SG_LEAD>(bf + TILE_U4, lane, g4, pb_hi, pb_lo, st.acc);
+    }
     convert_tile8(lds + ((j + 1) % STAGES) * STAGE8_U4, bfp + ((j + 1) & 1) * STAGE_U4);
-    if (p0 >= Lwave) continue;
-    const u32x4_t* bf = bfp + (j & 1) * STAGE_U4;
-    f32x4_t sacc[NT][2];
-    tile::qk_tile<NT, NT == 1, SG_LEAD>(bf, qb, c, g4, sacc);
-    u32x4_t pb_hi[NT], pb_lo[NT];
-    tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc, pb_hi,
-                                        pb_lo);
-    tile::pv_tile_tr<NT, SPLIT, NT == 1, SG_LEAD>(bf + TILE_U4, lane, g4, pb_hi, pb_lo, st.acc);
   }
 }
 
@@ -381,12 +383,14 @@ __device__ __forceinline__ void run_tiles_bal(int j0, int j1, int Lwave, u32x4_t
 
 // run_tiles_bal on the fp8 cache: the fp8 ring and the double-buffered bf16 pair of
 // run_tiles8, loaded and converted by the first 8 waves (LOAD; 512 threads, one 16-byte chunk of
-// K and of V each), one tile ahead: iteration j converts tile j + 1 into pair (j + 1) % 2 while
-// every wave computes tile j from pair j % 2, so one barrier per tile serves both (the tile
+// K and of V each), one tile ahead: iteration j computes tile j from pair j % 2, then the loading
+// waves convert tile j + 1 into pair (j + 1) % 2, so one barrier per tile serves both (the tile
 // converted before the barrier of iteration j is tile j). Tile j's fp8 stage is free once it has
 // been converted, so iteration j refills it with tile j + STAGES: loads still run STAGES - 1
-// iterations ahead of their conversion. Same bits; config 5 fp8 188.3 -> 182.9 us with the rank
-// rule of the bf16 instance (the convert-then-barrier-then-compute loop: 188.3 / 186.5).
+// iterations ahead of their conversion. Same bits; config 5 fp8, one-process A/Bs in us per call:
+// converting tile j between two barriers, then computing it, 188.3 (186.5 with this rule);
+// converting tile j + 1 before the arithmetic 182.9; after it 169.9 against 180.3 (166.6 against
+// 178.2 on another box).
 template <bool SPLIT, bool MASK, bool LOAD>
 __device__ __forceinline__ void run_tiles_bal8(int j0, int j1, int Lwave, u32x4_t* lds,
                                                __amdgpu_buffer_rsrc_t krs,
@@ -400,13 +404,12 @@ __device__ __forceinline__ void run_tiles_bal8(int j0, int j1, int Lwave, u32x4_
     vmcnt_wait<LOADS_PER_TILE8 * (STAGES - 2)>();  // this wave's loads of tile j + 1 are done
     // ... and every wave's; bf16 tile j is complete, tile j's fp8 stage and pair (j + 1) % 2 free
     __syncthreads();
-    if (LOAD) {
-      issue_tile8(lds + (j % STAGES) * STAGE8_U4, krs, vrs, p0 + STAGES * BN, w, lane);
-      convert_tile8(lds + ((j + 1) % STAGES) * STAGE8_U4, bfp + ((j + 1) & 1) * STAGE_U4);
+    if (LOAD) issue_tile8(lds + (j % STAGES) * STAGE8_U4, krs, vrs, p0 + STAGES * BN, w, lane);
+    if (p0 < Lwave) {
+      const u32x4_t* bf = bfp + (j & 1) * STAGE_U4;
+      tile_math_bal<SPLIT, MASK>(bf, bf + TILE_U4, p0, lane, c, g4, qb, Lcol, scale_log2, st);
     }
-    if (p0 >= Lwave) continue;
-    const u32x4_t* bf = bfp + (j & 1) * STAGE_U4;
-    tile_math_bal<SPLIT, MASK>(bf, bf + TILE_U4, p0, lane, c, g4, qb, Lcol, scale_log2, st);
+    if (LOAD) convert_tile8(lds + ((j + 1) % STAGES) * STAGE8_U4, bfp + ((j + 1) & 1) * STAGE_U4);
   }
 }
 
