@@ -359,7 +359,10 @@ __device__ __forceinline__ void tile_math_bal(const u32x4_t* kt, const u32x4_t* 
 
 // LOAD: this wave is one of the first 8, which fill the ring. The loaders and the other 4 waves
 // run separate copies of the loop, so neither carries the other's code (config 5: 212.8 -> 191.9
-// us on one box against the same loop with a per-wave branch around the loads, same bits).
+// us on one box against the same loop with a per-wave branch around the loads, same bits). The
+// loaders issue the next tile after their arithmetic on this one (the stage is free from the
+// barrier on): 158.2 -> 156.8 us against issuing it first (one-process A/Bs, same bits; in the
+// fp8 loop the same move measured 171.5 -> 173.2).
 template <bool SPLIT, bool MASK, bool LOAD>
 __device__ __forceinline__ void run_tiles_bal(int j0, int j1, int Lwave, u32x4_t* lds,
                                               __amdgpu_buffer_rsrc_t krs,
@@ -373,11 +376,10 @@ __device__ __forceinline__ void run_tiles_bal(int j0, int j1, int Lwave, u32x4_t
     const int p0 = j * BN;
     vmcnt_wait<LOADS_PER_TILE * (BAL_AHEAD - 1)>();  // this wave's loads of tile j are done
     __syncthreads();  // ... and every wave's; the stage refilled now (tile j-2's) is free
+    if (p0 < Lwave) tile_math_bal<SPLIT, MASK>(kt, vt, p0, lane, c, g4, qb, Lcol, scale_log2, st);
     if (LOAD)
       issue_tile(lds + ((j + BAL_AHEAD) % STAGES) * STAGE_U4, krs, vrs, p0 + BAL_AHEAD * BN, w,
                  lane);
-    if (p0 >= Lwave) continue;
-    tile_math_bal<SPLIT, MASK>(kt, vt, p0, lane, c, g4, qb, Lcol, scale_log2, st);
   }
 }
 
