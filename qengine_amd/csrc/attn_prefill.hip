@@ -107,15 +107,18 @@ __device__ __forceinline__ void run_tiles(int j0, int j1, int Lwave, u32x4_t* ld
     const int p0 = j * BN;
     vmcnt_wait<LOADS_PER_TILE * (AHEAD - 1)>();  // this wave's loads of tile j are done
     __syncthreads();                // ... and every wave's; tile j-1's stage is free
-    if (w < WAVES)                  // the first WAVES waves load the ring
+    // the arithmetic on tile j first, then the loads of tile j + AHEAD: GQA 4 / 8 shapes of
+    // config 5 231.3 / 145.0 -> 225.6 / 140.0 us against issuing the loads first (same bits)
+    if (p0 < Lwave) {  // tiles past this wave's rows contribute nothing
+      f32x4_t sacc[NT][2];
+      tile::qk_tile<NT, NT == 1, SG_LEAD>(kt, qb, c, g4, sacc);
+      u32x4_t pb_hi[NT], pb_lo[NT];
+      tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc,
+                                          pb_hi, pb_lo);
+      tile::pv_tile_tr<NT, SPLIT, NT == 1, SG_LEAD>(vt, lane, g4, pb_hi, pb_lo, st.acc);
+    }
+    if (w < WAVES)  // the first WAVES waves load the ring
       issue_tile(lds + ((j + AHEAD) % STAGES) * STAGE_U4, krs, vrs, p0 + AHEAD * BN, w, lane);
-    if (p0 >= Lwave) continue;      // tiles past this wave's rows contribute nothing
-    f32x4_t sacc[NT][2];
-    tile::qk_tile<NT, NT == 1, SG_LEAD>(kt, qb, c, g4, sacc);
-    u32x4_t pb_hi[NT], pb_lo[NT];
-    tile::softmax_tile<NT, MASK, SPLIT>(sacc, p0, Lcol, scale_log2, g4, st.m, st.l, st.acc, pb_hi,
-                                        pb_lo);
-    tile::pv_tile_tr<NT, SPLIT, NT == 1, SG_LEAD>(vt, lane, g4, pb_hi, pb_lo, st.acc);
   }
 }
 
